@@ -1,0 +1,156 @@
+// The `feather_ops` torch library and the `feather_ops._C` Python module (reference: csrc/extension.cpp:1-23
+// plus the op registration of csrc/hip_kernel.cu:716-846). Host code only: it validates the tensors,
+// takes the current stream of a's device, and calls the C ABI of libfeather_ops_gfx950.so
+// (include/feather_ops.h). Built against torch's stable ABI, like the reference.
+#include <Python.h>
+
+#include <torch/csrc/stable/accelerator.h>
+#include <torch/csrc/stable/library.h>
+#include <torch/csrc/stable/tensor.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <optional>
+
+#include "feather_ops.h"
+
+namespace {
+
+using torch::stable::Tensor;
+using ST = torch::headeronly::ScalarType;
+
+bool is_aligned(const void* p, uintptr_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+}
+
+// feather_ops::scaled_mm. Preconditions and messages follow csrc/hip_kernel.cu:729-801; N is relaxed from
+// a multiple of 16 to a multiple of 8 (16-byte output rows stay aligned, partial 16-column tiles are masked).
+void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
+               const std::optional<Tensor>& bias, Tensor& c, const int64_t block_warps_m, const int64_t block_warps_n,
+               const int64_t unroll_k, const int64_t repeat_m, const int64_t repeat_n, const bool prefetch) {
+    STD_TORCH_CHECK(a.is_cuda(), "a must be a CUDA tensor");
+    STD_TORCH_CHECK(b_prepacked.is_cuda(), "b_prepacked must be a CUDA tensor");
+    STD_TORCH_CHECK(c.is_cuda(), "c must be a CUDA tensor");
+    const auto device_index = a.get_device_index();
+    STD_TORCH_CHECK(b_prepacked.get_device_index() == device_index, "b_prepacked must be on the same device as a");
+    STD_TORCH_CHECK(c.get_device_index() == device_index, "c must be on the same device as a");
+
+    const auto a_type = a.scalar_type();
+    STD_TORCH_CHECK(a_type == ST::Half || a_type == ST::BFloat16, "a must be float16 or bfloat16");
+    STD_TORCH_CHECK(c.scalar_type() == ST::Half || c.scalar_type() == ST::BFloat16, "c must be float16 or bfloat16");
+    const auto b_type = b_prepacked.scalar_type();
+    STD_TORCH_CHECK(b_type == ST::Float8_e4m3fn || b_type == ST::Float8_e5m2,
+                    "b_prepacked must be float8_e4m3fn or float8_e5m2");
+
+    STD_TORCH_CHECK(a.dim() == 2, "a must be 2D");
+    STD_TORCH_CHECK(b_prepacked.dim() == 3, "b_prepacked must be 3D (K/16, N, 16)");
+    STD_TORCH_CHECK(c.dim() == 2, "c must be 2D");
+
+    const int64_t M = a.size(0);
+    const int64_t K = a.size(1);
+    const int64_t N = b_prepacked.size(1);
+    STD_TORCH_CHECK(K % 16 == 0, "K must be divisible by 16");
+    STD_TORCH_CHECK(K >= 16, "K must be at least 16");
+    STD_TORCH_CHECK(N % 8 == 0, "N must be divisible by 8");
+    STD_TORCH_CHECK(b_prepacked.size(0) >= K / 16, "b_prepacked.shape[0] must be at least K/16 (", K / 16, ")");
+    STD_TORCH_CHECK(b_prepacked.size(0) % 8 == 0, "b_prepacked.shape[0] must be a multiple of 8 (K padded to 128)");
+    STD_TORCH_CHECK(b_prepacked.size(2) == 16, "b_prepacked.shape[2] must be 16");
+    STD_TORCH_CHECK(c.size(0) == M, "c.shape[0] must equal M");
+    STD_TORCH_CHECK(c.size(1) == N, "c.shape[1] must equal N");
+
+    STD_TORCH_CHECK(a.stride(0) == K, "a.stride(0) must equal K (", K, ")");
+    STD_TORCH_CHECK(a.stride(1) == 1, "a.stride(1) must be 1");
+    STD_TORCH_CHECK(b_prepacked.stride(0) == N * 16, "b_prepacked.stride(0) must equal N*16 (", N * 16, ")");
+    STD_TORCH_CHECK(b_prepacked.stride(1) == 16, "b_prepacked.stride(1) must be 16");
+    STD_TORCH_CHECK(b_prepacked.stride(2) == 1, "b_prepacked.stride(2) must be 1");
+    STD_TORCH_CHECK(c.stride(0) == N, "c.stride(0) must equal N (", N, ")");
+    STD_TORCH_CHECK(c.stride(1) == 1, "c.stride(1) must be 1");
+
+    if (scale.has_value()) {
+        const Tensor& s = *scale;
+        STD_TORCH_CHECK(s.is_cuda(), "scale must be a CUDA tensor");
+        STD_TORCH_CHECK(s.get_device_index() == device_index, "scale must be on the same device as a");
+        STD_TORCH_CHECK(s.scalar_type() == ST::Float, "scale must be float32");
+        STD_TORCH_CHECK(s.numel() == 1, "scale must have one element");
+    }
+    if (bias.has_value()) {
+        const Tensor& b = *bias;
+        STD_TORCH_CHECK(b.is_cuda(), "bias must be a CUDA tensor");
+        STD_TORCH_CHECK(b.get_device_index() == device_index, "bias must be on the same device as a");
+        STD_TORCH_CHECK(b.scalar_type() == c.scalar_type(), "bias must have the same dtype as c");
+        STD_TORCH_CHECK(b.numel() == N, "bias must have N elements");
+        STD_TORCH_CHECK(b.numel() == 0 || b.stride(b.dim() - 1) == 1, "bias must be contiguous");
+        STD_TORCH_CHECK(is_aligned(b.const_data_ptr(), 8), "bias data pointer must be 8-byte aligned");
+    }
+
+    const int64_t threads = 64 * block_warps_m * block_warps_n;
+    STD_TORCH_CHECK(threads <= 1024, "Block size exceeds HIP thread-per-block limit");
+    STD_TORCH_CHECK(M * K * 2 < (int64_t{1} << 31) && M * N * 2 < (int64_t{1} << 31) &&
+                        b_prepacked.size(0) * N * 16 < (int64_t{1} << 31),
+                    "a, b_prepacked and c must each be smaller than 2 GiB");
+    if (M == 0) return;
+
+    torch::stable::accelerator::DeviceGuard guard(device_index);
+    void* raw_stream = nullptr;
+    TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &raw_stream));
+
+    STD_TORCH_CHECK(is_aligned(a.const_data_ptr(), 16), "a data pointer must be 16-byte aligned");
+    STD_TORCH_CHECK(is_aligned(b_prepacked.const_data_ptr(), 16), "b_prepacked data pointer must be 16-byte aligned");
+    STD_TORCH_CHECK(is_aligned(c.mutable_data_ptr(), 16), "c data pointer must be 16-byte aligned");
+
+    const bool launched = launch_scaled_mm(
+        static_cast<const uint16_t*>(a.const_data_ptr()), static_cast<const uint8_t*>(b_prepacked.const_data_ptr()),
+        scale.has_value() ? static_cast<const float*>(scale->const_data_ptr()) : nullptr,
+        bias.has_value() ? static_cast<const uint16_t*>(bias->const_data_ptr()) : nullptr,
+        static_cast<uint16_t*>(c.mutable_data_ptr()), M, N, K, scale.has_value() ? 1 : 0, bias.has_value() ? 1 : 0,
+        b_type == ST::Float8_e5m2, a_type == ST::BFloat16, c.scalar_type() == ST::BFloat16,
+        static_cast<int>(block_warps_m), static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
+        static_cast<int>(repeat_m), static_cast<int>(repeat_n), prefetch, static_cast<hipStream_t>(raw_stream));
+    STD_TORCH_CHECK(launched, "Unsupported config");
+    const hipError_t err = hipGetLastError();
+    STD_TORCH_CHECK(err == hipSuccess, "scaled_mm kernel launch failed: ", hipGetErrorString(err));
+}
+
+// feather_ops::bf16_to_fp16: out = bf16 -> fp16 (round toward zero) of x, both contiguous on one device.
+void bf16_to_fp16(const Tensor& x, Tensor& out) {
+    STD_TORCH_CHECK(x.is_cuda() && out.is_cuda(), "x and out must be CUDA tensors");
+    STD_TORCH_CHECK(x.get_device_index() == out.get_device_index(), "x and out must be on one device");
+    STD_TORCH_CHECK(x.scalar_type() == ST::BFloat16, "x must be bfloat16");
+    STD_TORCH_CHECK(out.scalar_type() == ST::Half, "out must be float16");
+    STD_TORCH_CHECK(x.is_contiguous() && out.is_contiguous(), "x and out must be contiguous");
+    STD_TORCH_CHECK(x.numel() == out.numel(), "x and out must have the same number of elements");
+    STD_TORCH_CHECK(x.numel() < (int64_t{1} << 30), "x must have fewer than 2^30 elements");
+    if (x.numel() == 0) return;
+    STD_TORCH_CHECK(is_aligned(x.const_data_ptr(), 16) && is_aligned(out.mutable_data_ptr(), 16),
+                    "x and out data pointers must be 16-byte aligned");
+    const auto device_index = x.get_device_index();
+    torch::stable::accelerator::DeviceGuard guard(device_index);
+    void* raw_stream = nullptr;
+    TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &raw_stream));
+    const bool launched = feather_bf16_to_fp16(static_cast<const uint16_t*>(x.const_data_ptr()),
+                                               static_cast<uint16_t*>(out.mutable_data_ptr()), x.numel(),
+                                               static_cast<hipStream_t>(raw_stream));
+    STD_TORCH_CHECK(launched, "bf16_to_fp16: unsupported arguments");
+    const hipError_t err = hipGetLastError();
+    STD_TORCH_CHECK(err == hipSuccess, "bf16_to_fp16 kernel launch failed: ", hipGetErrorString(err));
+}
+
+}  // namespace
+
+STABLE_TORCH_LIBRARY(feather_ops, m) {
+    m.def(
+        "scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, int block_warps_m, "
+        "int block_warps_n, int unroll_k, int repeat_m, int repeat_n, bool prefetch) -> ()");
+    m.def("bf16_to_fp16(Tensor x, Tensor(a!) out) -> ()");
+}
+
+STABLE_TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
+    m.impl("scaled_mm", TORCH_BOX(&scaled_mm));
+    m.impl("bf16_to_fp16", TORCH_BOX(&bf16_to_fp16));
+}
+
+extern "C" PyObject* PyInit__C(void) {
+    static PyModuleDef module = {PyModuleDef_HEAD_INIT, "_C", nullptr, -1, nullptr, nullptr, nullptr, nullptr, nullptr};
+    return PyModule_Create(&module);
+}

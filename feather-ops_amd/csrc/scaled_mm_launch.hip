@@ -1,0 +1,51 @@
+// Instantiates every tile of feather_tiles.h for ONE (weight format, activation dtype, output dtype)
+// combination and dispatches a tile query to it. The build compiles this file once per combination,
+// with FEATHER_B_E5M2, FEATHER_A_BF16 and FEATHER_OUT_BF16 set to 0 or 1, so the eight combinations
+// compile in parallel. The instantiation flow (X-macro tile list -> template per tile) follows the
+// reference's dispatch_scaled_mm (csrc/hip_kernel.cu:668-684).
+#include "scaled_mm_launch.h"
+
+#include "feather_tiles.h"
+#include "scaled_mm_kernels.h"
+
+#if !defined(FEATHER_B_E5M2) || !defined(FEATHER_A_BF16) || !defined(FEATHER_OUT_BF16)
+#error "compile with -DFEATHER_B_E5M2=<0|1> -DFEATHER_A_BF16=<0|1> -DFEATHER_OUT_BF16=<0|1>"
+#endif
+
+namespace feather {
+namespace {
+
+constexpr bool kE5M2 = FEATHER_B_E5M2 != 0;
+constexpr bool kABf16 = FEATHER_A_BF16 != 0;
+constexpr bool kOutBf16 = FEATHER_OUT_BF16 != 0;
+
+template <int WM, int WN, int U, int RM, int RN, int PF>
+bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
+    if (t.warps_m != WM || t.warps_n != WN || t.unroll_k != U || t.repeat_m != RM || t.repeat_n != RN ||
+        t.prefetch != (PF != 0)) {
+        return false;
+    }
+    if constexpr (PF != 0) {
+        using S = RingShape<WM, WN, U, RM, RN>;
+        const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
+        hipLaunchKernelGGL((ring_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
+                           dim3(S::kThreads), 0, stream, p);
+    } else {
+        using S = StreamShape<WM, WN, U, RM, RN>;
+        const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
+        hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
+                           dim3(S::kThreads), 0, stream, p);
+    }
+    return true;
+}
+
+}  // namespace
+
+bool FEATHER_COMBO_FN(FEATHER_B_E5M2, FEATHER_A_BF16, FEATHER_OUT_BF16)(const TileQuery& t, const Params& p,
+                                                                          hipStream_t stream) {
+#define FEATHER_TRY_TILE(wm, wn, u, rm, rn, pf) || try_tile<wm, wn, u, rm, rn, pf>(t, p, stream)
+    return false FEATHER_SCALED_MM_TILES(FEATHER_TRY_TILE);
+#undef FEATHER_TRY_TILE
+}
+
+}  // namespace feather

@@ -1,0 +1,132 @@
+"""Mixed-precision matmul against a prepacked fp8 weight on gfx950: `Y = (X @ W^T) * scale + bias`.
+
+Drop-in for the reference's `feather_ops/scaled_mm.py` (same names, arguments and op boundary):
+`X` is fp16 or bf16 `[M, K]`, `W` is fp8e5m2 or fp8e4m3fn stored as `[K_pad/16, N, 16]` (see
+`prepack_b_for_scaled_mm`), `scale` is a per-tensor fp32 scalar on the device and `bias` is optional. The
+output is fp16 or bf16. Any `M >= 1` works, with `K` a multiple of 16 and `N` a multiple of 8 (the
+reference needs 16).
+
+Numerics are the naive path's (`feather_ops/naive.py:4-41`) with fp32 accumulation: bf16 activations are
+widened to fp16 (RNE), the weight decodes exactly to fp16, the MFMAs accumulate in fp32, the scale is
+applied in fp32, the downcast rounds to nearest even, and the bias is added in the output precision.
+
+`scaled_mm_hip` picks the tile with the static heuristic below and hands it to the kernel through an
+opaque custom op, so `torch.compile` sees one node whatever the shape (reference `scaled_mm.py:104-114`).
+Pass `tile=` to pin it, which is what the benchmark sweeps and the tests do.
+"""
+
+import torch
+from torch.library import custom_op
+
+from . import _lib
+from .tiles import gemm_block_sizes
+
+# Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
+_TILE_STREAM_16x64 = (4, 1, 4, 1, 4, 0)
+_TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
+_TILE_STREAM_64x64 = (2, 2, 4, 4, 2, 0)
+_TILE_64x64 = (2, 2, 4, 2, 2, 1)
+_TILE_128x128 = (2, 2, 4, 4, 4, 1)
+_TILE_128x256 = (2, 4, 4, 4, 4, 1)
+_TILE_256x256 = (2, 4, 4, 8, 4, 1)
+
+# MI355X: 256 compute units. A launch below about one block per CU leaves the machine partly idle.
+_CUS = 256
+
+
+def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
+    bm, bn, _ = gemm_block_sizes(tile)
+    return -(-M // bm) * -(-N // bn)
+
+
+def select_scaled_mm_config(
+    M: int,
+    N: int,
+    K: int,
+    a_dtype: torch.dtype = torch.float16,
+    b_dtype: torch.dtype = torch.float8_e5m2,
+    out_dtype: torch.dtype = torch.bfloat16,
+) -> tuple[int, int, int, int, int, int]:
+    """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
+
+    Skinny M streams the weight through registers with K split across waves (the weight read is the
+    whole cost there); from 65 rows up the LDS ring takes over, and the tallest tile whose grid still
+    covers the 256 CUs wins, since a bigger tile re-reads fewer panels per FLOP.
+    """
+    del K, a_dtype, b_dtype, out_dtype
+    if M <= 16:
+        return _TILE_STREAM_16x64
+    if M <= 32:
+        return _TILE_STREAM_32x64
+    if M <= 64:
+        return _TILE_STREAM_64x64
+    for tile in (_TILE_256x256, _TILE_128x256, _TILE_128x128):
+        if _blocks(M, N, tile) >= _CUS:
+            return tile
+    return _TILE_128x128 if _blocks(M, N, _TILE_128x128) >= _CUS // 2 else _TILE_64x64
+
+
+def _launch(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out: torch.Tensor,
+    tile: tuple[int, int, int, int, int, int],
+) -> None:
+    torch.ops.feather_ops.scaled_mm.default(a, b_prepacked, scale, bias, out, *tile)
+
+
+@custom_op("feather_ops::scaled_mm_auto", mutates_args=("out",))
+def _scaled_mm_auto(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out: torch.Tensor,
+) -> None:
+    """The heuristic behind an opaque boundary: `torch.compile` does not specialize on its branches."""
+    tile = select_scaled_mm_config(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype, b_prepacked.dtype, out.dtype)
+    _launch(a, b_prepacked, scale, bias, out, tile)
+
+
+def scaled_mm_hip(
+    a: torch.Tensor,
+    b_prepacked: torch.Tensor,
+    scale: torch.Tensor | None,
+    bias: torch.Tensor | None,
+    out_dtype: torch.dtype,
+    tile: tuple[int, int, int, int, int, int] | None = None,
+) -> torch.Tensor:
+    """`(a @ b^T) * scale + bias` against the prepacked fp8 weight `b_prepacked`.
+
+    `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it.
+    """
+    _lib.require_native()
+    out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
+    if tile is None:
+        _scaled_mm_auto(a, b_prepacked, scale, bias, out)
+    else:
+        _launch(a, b_prepacked, scale, bias, out, tile)
+    return out
+
+
+def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
+    """`[K, N]` fp8 -> `[K_pad/16, N, 16]`, the layout the kernel indexes (reference `scaled_mm.py:137-150`).
+
+    `K` is zero-padded to a multiple of 128, so a ragged K never needs a staging branch; element
+    `[k // 16, n, k % 16]` of the result is `b[k, n]`. Runs as torch copy kernels on `b`'s device, once
+    per weight.
+    """
+    k, n = b.shape
+    k_pad = -(-k // 128) * 128
+    if k_pad != k:
+        padded = torch.zeros((k_pad, n), device=b.device, dtype=b.dtype)
+        padded[:k] = b
+        b = padded
+    return b.view(k_pad // 16, 16, n).permute(0, 2, 1).contiguous()
+
+
+def tile_shape(tile: tuple[int, ...]) -> tuple[int, int, int]:
+    """`(block_m, block_n, chunk_k)` of a tile."""
+    return gemm_block_sizes(tile)

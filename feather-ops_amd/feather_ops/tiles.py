@@ -1,0 +1,55 @@
+"""The instantiated scaled_mm tiles for gfx950, and the tile vocabulary the heuristic chooses from.
+
+This file is the single source of truth: `feather-ops_amd/gen_tiles.py` renders `SCALED_MM_TILES` into
+`csrc/feather_tiles.h`, which the HIP sources use to instantiate and dispatch, so every tile the
+heuristic can return is a compiled kernel (same flow as the reference's `feather_ops/tiles.py:1-15` ->
+`tools/gen_tiles.py` -> `csrc/feather_tiles.h`). It must not import torch: the build reads it before the
+extension exists.
+
+Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, repeat_n, prefetch)`
+(`tiles.py:8-12`, op schema `csrc/hip_kernel.cu:827-840`), re-interpreted for CDNA4's wave64 MFMA:
+
+- A wave is 64 lanes and an MFMA fragment is 16 x 16 outputs (`v_mfma_f32_16x16x32_f16`), so
+  `block_m = 16 * warps_m * repeat_m`, `block_n = 16 * warps_n * repeat_n` and `chunk_k = 16 * unroll_k`
+  keep their meaning; `unroll_k` must be a multiple of 4 (whole 64-deep MFMA groups).
+- `prefetch = 1` selects the LDS ring kernel: `warps_m x warps_n` waves each own a
+  `16*repeat_m x 16*repeat_n` sub-tile, and K streams through a double-buffered LDS ring of `chunk_k`-deep
+  stages whose next stage is in flight while the current one feeds the MFMAs.
+- `prefetch = 0` selects the streaming kernel for skinny M: no LDS staging. The block's `warps_m` waves
+  split K instead of M (so `block_m = 16 * repeat_m`), its `warps_n` waves split N, and each wave streams
+  its operands from HBM into registers `chunk_k` at a time, double-buffered; a short LDS reduction joins
+  the K slices in a fixed order.
+"""
+
+SCALED_MM_TILES = [
+    # LDS ring (prefetch = 1)
+    (2, 4, 4, 8, 4, 1),  # 256 x 256, 8 waves of 128 x 64
+    (4, 2, 4, 4, 8, 1),  # 256 x 256, 8 waves of 64 x 128
+    (2, 4, 4, 4, 4, 1),  # 128 x 256
+    (4, 2, 4, 4, 4, 1),  # 256 x 128
+    (2, 2, 4, 4, 4, 1),  # 128 x 128
+    (2, 2, 8, 4, 4, 1),  # 128 x 128, 128-deep stages
+    (1, 4, 4, 4, 2, 1),  # 64 x 128
+    (2, 2, 4, 2, 2, 1),  # 64 x 64
+    # streaming split-K (prefetch = 0)
+    (4, 1, 4, 1, 4, 0),  # 16 x 64, 4 K slices
+    (4, 1, 8, 1, 4, 0),  # 16 x 64, 4 K slices, 128-deep steps
+    (8, 1, 4, 1, 4, 0),  # 16 x 64, 8 K slices
+    (4, 2, 4, 1, 2, 0),  # 16 x 64, 4 K slices x 2 column waves
+    (4, 1, 4, 1, 2, 0),  # 16 x 32
+    (2, 2, 4, 2, 2, 0),  # 32 x 64
+    (2, 2, 4, 4, 2, 0),  # 64 x 64
+]
+
+
+def gemm_block_sizes(tile: tuple[int, ...]) -> tuple[int, int, int]:
+    """`(block_m, block_n, chunk_k)` of a `SCALED_MM_TILES` entry."""
+    warps_m, warps_n, unroll_k, repeat_m, repeat_n = tile[:5]
+    prefetch = tile[5] if len(tile) > 5 else 1
+    block_m = 16 * repeat_m if prefetch == 0 else 16 * warps_m * repeat_m
+    return block_m, 16 * warps_n * repeat_n, 16 * unroll_k
+
+
+def threads_per_block(tile: tuple[int, ...]) -> int:
+    """Work-items of one block: 64 per wave, `warps_m * warps_n` waves."""
+    return 64 * tile[0] * tile[1]

@@ -1,0 +1,59 @@
+/*
+ * C ABI of the gfx950 scaled matmul library (libfeather_ops_gfx950.so). Plain pointers and sizes, no
+ * torch types: this is the boundary a C/C++ benchmark, a ctypes/cffi binding or the thin torch extension
+ * (feather-ops_amd/csrc/extension.cpp) binds.
+ */
+#ifndef FEATHER_OPS_H
+#define FEATHER_OPS_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same declaration as <hip/hip_runtime_api.h>, so this header needs no HIP include. */
+typedef struct ihipStream_t* hipStream_t;
+
+/*
+ * c[M, N] = round_out((a[M, K] @ decode(b)) * scale) (+ bias), enqueued on `stream` (asynchronous).
+ *
+ * Replaces the reference's `extern "C" bool launch_scaled_mm(...)` (csrc/hip_kernel.cu:687-713), as
+ * declared by its consumer cpp_benchmarks/benchmark_scaled_mm_hip.cpp:27-47: same symbol, same arguments.
+ *
+ *   a            [M, K] row-major, fp16 bits (a_bf16 = false) or bf16 bits (a_bf16 = true); bf16 is
+ *                widened to fp16 with round-to-nearest-even, as feather_ops/naive.py:21 does.
+ *   b_prepacked  [K_pad/16, N, 16] fp8 codes, e5m2 (use_fp8_e5m2 = true) or e4m3fn (false), K_pad a
+ *                multiple of 128 with zero pad rows (feather_ops/scaled_mm.py:137-150).
+ *   scale        one fp32 value in device memory, read by the kernel (has_scale != 0), or ignored.
+ *   bias         N values of the output dtype (has_bias != 0), added after the downcast, or ignored.
+ *   c            [M, N] row-major output, fp16 (output_bf16 = false) or bf16 (true), rounded to nearest even.
+ *   tile         (block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch): one entry of
+ *                feather_ops/tiles.py SCALED_MM_TILES (gfx950 meaning documented there).
+ *
+ * Contract (checked here; a violation returns false and enqueues nothing): M >= 1, N >= 1 with
+ * N % 8 == 0 (the reference requires N % 16 == 0), K >= 16 with K % 16 == 0, a, b_prepacked and c
+ * 16-byte aligned, bias 8-byte aligned, a/c/b_prepacked each under 2 GiB. The kernel reads
+ * b_prepacked rows up to ceil(K / 128) * 8. Returns false for a tile that is not instantiated (the
+ * reference's only false case) and true once the kernel is enqueued; launch errors are left to the
+ * caller (hipGetLastError), as in the reference.
+ */
+bool launch_scaled_mm(const uint16_t* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                      uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias,
+                      bool use_fp8_e5m2, bool a_bf16, bool output_bf16, int block_warps_m, int block_warps_n,
+                      int unroll_k, int repeat_m, int repeat_n, bool prefetch, hipStream_t stream);
+
+/*
+ * out[i] = bf16 -> fp16 of in[i] with round-toward-zero (finite overflow saturates to +-65504, inf/NaN
+ * pass through), n elements, enqueued on `stream`. Replaces the reference's Triton kernel behind
+ * feather_ops/convert.py:24-34 (bf16_to_fp16), which has no C entry point of its own. in/out 16-byte
+ * aligned, n < 2^30; returns false (nothing enqueued) otherwise.
+ */
+bool feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FEATHER_OPS_H */

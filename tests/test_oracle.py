@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it. CPU only.
+
+Each oracle function is checked against something that does not share its code: torch's casts (the
+library routines the reference's naive path calls), the reference's known-answer list, brute-force loops,
+closed forms, and golden fixtures computed from torch casts plus float64 numpy matmul
+(tests/golden/make_golden.py). The last tests plant mistakes in the oracle's inputs and check that the
+goldens catch them.
+"""
+
+import hashlib
+import json
+import math
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import naive as oracle
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def _golden():
+    data = np.load(GOLDEN / "golden.npz", allow_pickle=False)
+    cases = {}
+    for key in data.files:
+        case, field = key.split("/")
+        cases.setdefault(case, {})[field] = data[key]
+    return cases
+
+
+CASES = _golden()
+
+
+def _same_bits(x_f32: np.ndarray, y_f32: np.ndarray) -> bool:
+    """Equal values, NaN matching NaN."""
+    x = np.asarray(x_f32, dtype=np.float32)
+    y = np.asarray(y_f32, dtype=np.float32)
+    nan = np.isnan(x)
+    return bool(np.array_equal(nan, np.isnan(y)) and np.array_equal(x[~nan], y[~nan]))
+
+
+# ---- element casts ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt,dtype", [(oracle.E5M2, torch.float8_e5m2), (oracle.E4M3FN, torch.float8_e4m3fn)])
+def test_fp8_decode_all_codes_match_torch(fmt, dtype):
+    codes = np.arange(256, dtype=np.uint8)
+    mine = oracle.decode_fp8(codes, fmt)
+    theirs = torch.from_numpy(codes).view(dtype).to(torch.float32).numpy()
+    assert _same_bits(mine, theirs)
+    # signs of zero survive too
+    assert np.signbit(mine[0x80]) and not np.signbit(mine[0x00])
+
+
+def test_e5m2_decode_matches_reference_known_answers():
+    kat = json.loads((GOLDEN / "e5m2_kat.json").read_text())
+    for code, value in kat.items():
+        assert oracle.decode_fp8(np.array([int(code, 16)], np.uint8))[0] == value
+
+
+def test_e5m2_decode_is_the_high_byte_of_fp16():
+    """The byte move the kernel uses (csrc/hip_kernel.cu:95-102 in the reference) gives the same value."""
+    codes = np.arange(256, dtype=np.uint16)
+    as_f16 = (codes << 8).astype(np.uint16).view(np.float16).astype(np.float32)
+    assert _same_bits(oracle.decode_fp8(codes.astype(np.uint8)), as_f16)
+
+
+def test_e4m3fn_special_values():
+    d = oracle.decode_fp8(np.array([0x7F, 0xFF, 0x7E, 0x01, 0x08, 0x00], np.uint8), oracle.E4M3FN)
+    assert np.isnan(d[0]) and np.isnan(d[1])
+    assert d[2] == 448.0 and d[3] == 2.0**-9 and d[4] == 2.0**-6 and d[5] == 0.0
+
+
+def test_bf16_widening_all_codes_match_torch():
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    mine = oracle.widen_bf16_to_f16(codes)
+    theirs = torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16).to(torch.float16).view(torch.int16).numpy()
+    mine_f = mine.view(np.float16).astype(np.float32)
+    theirs_f = theirs.view(np.uint16).view(np.float16).astype(np.float32)
+    assert _same_bits(mine_f, theirs_f)
+    finite = np.isfinite(mine_f)
+    assert np.array_equal(mine[finite], theirs.view(np.uint16)[finite])  # bit-exact incl. signed zeros
+
+
+def _cast_sweep():
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.normal(size=20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65519.99, 65520.0, -65520.0, 1e30, np.inf, -np.inf, np.nan,
+                  2.0**-24, 2.0**-25, 3 * 2.0**-26, 2.0**-14, 2.0**-14 - 2.0**-25, 1.0 + 2.0**-11,
+                  1.0 + 3 * 2.0**-11, 1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8, 3.4e38, 1e-40], dtype=np.float32),
+    ])
+    # exact ties for both formats
+    m = rng.integers(1024, 2048, 500)
+    x = np.concatenate([x, ((m * 2 + 1) * 2.0 ** rng.integers(-20, 4, 500) / 2048).astype(np.float32)])
+    return x.astype(np.float32)
+
+
+def test_f32_to_f16_rne_matches_torch():
+    x = _cast_sweep()
+    mine = oracle.f32_to_f16(x).view(np.float16).astype(np.float32)
+    theirs = torch.from_numpy(x).to(torch.float16).to(torch.float32).numpy()
+    assert _same_bits(mine, theirs)
+
+
+def test_f32_to_bf16_rne_matches_torch():
+    x = _cast_sweep()
+    mine = oracle.bits_to_f32(oracle.f32_to_bf16(x), oracle.BF16)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    assert _same_bits(mine, theirs)
+
+
+# ---- layout ----------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("k,n", [(16, 8), (20 * 16, 3), (128, 24), (130 * 16, 5)])
+def test_prepack_brute_force(k, n):
+    rng = np.random.default_rng(k * 31 + n)
+    b = rng.integers(0, 256, size=(k, n), dtype=np.uint8)
+    p = oracle.prepack(b)
+    k_pad = -(-k // 128) * 128
+    assert p.shape == (k_pad // 16, n, 16)
+    for kk in range(k_pad):
+        for nn in range(n):
+            assert p[kk // 16, nn, kk % 16] == (b[kk, nn] if kk < k else 0)
+    assert np.array_equal(oracle.unpack(p, k), b)
+
+
+def test_prepack_matches_golden_loops():
+    for case in CASES.values():
+        if "packed" in case:
+            assert np.array_equal(oracle.prepack(case["b_codes"]), case["packed"])
+
+
+def test_product_prepack_matches_oracle_on_cpu():
+    """feather_ops.prepack_b_for_scaled_mm is device-agnostic torch code; check it on CPU tensors."""
+    from feather_ops.scaled_mm import prepack_b_for_scaled_mm
+
+    rng = np.random.default_rng(3)
+    for k, n in [(16, 8), (272, 304), (1024, 40)]:
+        b = rng.integers(0, 256, size=(k, n), dtype=np.uint8)
+        got = prepack_b_for_scaled_mm(torch.from_numpy(b).view(torch.float8_e5m2)).view(torch.uint8).numpy()
+        assert np.array_equal(got, oracle.prepack(b))
+
+
+# ---- the matmul: closed forms ----------------------------------------------------------------------------
+
+def _f16(x):
+    return torch.tensor(np.asarray(x, np.float32)).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_identity_weight_returns_scaled_activations():
+    k = 64
+    rng = np.random.default_rng(0)
+    a = _f16(rng.normal(size=(3, k)))
+    b = np.zeros((k, k), np.uint8)
+    b[np.arange(k), np.arange(k)] = 0x3C  # e5m2 1.0
+    out = oracle.scaled_mm(a, oracle.F16, oracle.prepack(b), oracle.E5M2, 0.25, None, oracle.F16)
+    want = (a.view(np.float16).astype(np.float32) * np.float32(0.25)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(out, want)
+
+
+def test_single_nonzero_picks_one_product():
+    k, n = 48, 24
+    rng = np.random.default_rng(1)
+    a = _f16(rng.normal(size=(5, k)))
+    b = np.zeros((k, n), np.uint8)
+    b[17, 11] = 0xBA  # -0.75
+    out = oracle.scaled_mm(a, oracle.F16, oracle.prepack(b), oracle.E5M2, None, None, oracle.F16)
+    af = a.view(np.float16).astype(np.float32)
+    want = np.zeros((5, n), np.float32)
+    want[:, 11] = af[:, 17] * np.float32(-0.75)
+    assert np.array_equal(out.view(np.float16).astype(np.float32), want.astype(np.float16).astype(np.float32))
+
+
+def test_zero_activations_give_bias():
+    k, n = 32, 16
+    b = np.random.default_rng(2).integers(0, 0x7B, size=(k, n), dtype=np.uint8)
+    bias = _f16(np.linspace(-3, 3, n))
+    out = oracle.scaled_mm(np.zeros((4, k), np.uint16), oracle.F16, oracle.prepack(b), oracle.E5M2, 3.0, bias,
+                           oracle.F16)
+    assert np.array_equal(out, np.broadcast_to(bias, (4, n)))
+
+
+def test_power_of_two_scale_is_exact_and_linear():
+    rng = np.random.default_rng(4)
+    a = _f16(rng.normal(size=(6, 96)))
+    b = torch.tensor(rng.normal(size=(96, 40)), dtype=torch.float32).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    p = oracle.prepack(b)
+    y1 = oracle.scaled_mm_f32(a, oracle.F16, p, oracle.E5M2, 1.0)
+    y8 = oracle.scaled_mm_f32(a, oracle.F16, p, oracle.E5M2, 8.0)
+    assert np.array_equal(y1 * 8, y8)
+
+
+def test_brute_force_float64_loops_tiny():
+    rng = np.random.default_rng(5)
+    m, k, n = 3, 32, 8
+    a = _f16(rng.normal(size=(m, k)))
+    codes = rng.integers(0, 0x7B, size=(k, n), dtype=np.uint8) | (rng.integers(0, 2, size=(k, n)) << 7).astype(np.uint8)
+    bias = _f16(rng.normal(size=n))
+    out = oracle.scaled_mm(a, oracle.F16, oracle.prepack(codes), oracle.E5M2, 0.1, bias, oracle.F16)
+    af = a.view(np.float16).astype(np.float64)
+    bf = codes.astype(np.uint16) << 8
+    bf = bf.view(np.float16).astype(np.float64)
+    for i in range(m):
+        for j in range(n):
+            s = 0.0
+            for kk in range(k):
+                s += af[i, kk] * bf[kk, j]
+            y = np.float16(np.float32(s) * np.float32(0.1))
+            y = np.float16(np.float32(y) + np.float32(bias.view(np.float16)[j]))
+            assert out[i, j] == np.array([y]).view(np.uint16)[0]
+
+
+def test_literal_fp16_accumulation_overflows_at_baseline_quantization():
+    """Why the oracle accumulates in fp32: naive.py:20-23's fp16 matmul overflows on C1's recipe."""
+    a_bits, packed, scale, b_codes = oracle.make_inputs(64, 1024, 256, oracle.F16, seed=0)
+    a16 = a_bits.view(np.float16)
+    b16 = (b_codes.astype(np.uint16) << 8).view(np.float16)
+    literal = oracle.literal_fp16_scaled_mm(a16, b16, scale)
+    assert np.isinf(literal).mean() > 0.5
+    fp32 = oracle.scaled_mm_f32(a_bits, oracle.F16, packed, oracle.E5M2, scale)
+    assert np.isfinite(fp32).all()
+
+
+# ---- the matmul: golden fixtures -------------------------------------------------------------------------
+
+SMALL = [name for name, c in CASES.items() if "a_bits" in c]
+
+
+def _run_case(case, a_bits=None, packed=None):
+    meta = json.loads(str(case["meta"]))
+    return oracle.scaled_mm(
+        case["a_bits"] if a_bits is None else a_bits, meta["a_fmt"],
+        case["packed"] if packed is None else packed, meta["b_fmt"], meta["scale"],
+        case.get("bias"), meta["out_fmt"],
+    ), meta
+
+
+@pytest.mark.parametrize("name", SMALL)
+def test_golden_small_cases_bit_exact(name):
+    case = CASES[name]
+    out, meta = _run_case(case)
+    want = case["out"]
+    got_f = oracle.bits_to_f32(out, meta["out_fmt"])
+    want_f = oracle.bits_to_f32(want, meta["out_fmt"])
+    assert _same_bits(got_f, want_f), name
+    finite = np.isfinite(want_f)
+    assert np.array_equal(out[finite], want[finite])
+
+
+def test_golden_specials_have_nan_and_inf():
+    out, meta = _run_case(CASES["specials_f16"])
+    f = oracle.bits_to_f32(out, meta["out_fmt"])
+    assert np.isnan(f).any() and np.isinf(f).any() and np.isfinite(f).any()
+    out, meta = _run_case(CASES["bf16_overflow"])
+    f = oracle.bits_to_f32(out, meta["out_fmt"])
+    assert not np.isfinite(f[0]).any() and np.isfinite(f[1:]).all()
+
+
+@pytest.mark.parametrize("name,outliers", [("c1_rows", False), ("c5_rows", True)])
+def test_golden_baseline_rows(name, outliers):
+    case = CASES[name]
+    meta = json.loads(str(case["meta"]))
+    a_bits, packed, scale, _ = oracle.make_inputs(meta["m"], meta["k"], meta["n"], meta["a_fmt"], seed=meta["seed"],
+                                                  outliers=outliers)
+    assert hashlib.sha256(a_bits.tobytes()).hexdigest() == meta["a_sha256"], "input recipe drifted"
+    assert hashlib.sha256(packed.tobytes()).hexdigest() == meta["packed_sha256"], "input recipe drifted"
+    assert math.isclose(scale, meta["scale"], rel_tol=0, abs_tol=0)
+    out = oracle.scaled_mm(a_bits, meta["a_fmt"], packed, oracle.E5M2, scale, None, meta["out_fmt"],
+                           rows=case["rows"], threads=4)
+    assert np.array_equal(out, case["out"])
+
+
+# ---- planted mistakes: the goldens must catch them ----------------------------------------------------------
+
+def test_golden_catches_a_transposed_weight():
+    case = CASES["tiny_f16"]
+    codes = case["b_codes"]  # [48, 24]: swap the column order as a transposition would scramble it
+    wrong = oracle.prepack(np.ascontiguousarray(codes[:, ::-1]))
+    out, _ = _run_case(case, packed=wrong)
+    assert not np.array_equal(out, case["out"])
+
+
+def test_golden_catches_a_dropped_k_term():
+    case = CASES["tiny_bf16_bf16out"]
+    a = case["a_bits"].copy()
+    a[:, 63] = 0  # drop the last k term
+    out, _ = _run_case(case, a_bits=a)
+    assert not np.array_equal(out, case["out"])
+
+
+def test_golden_catches_a_wrong_chunk_order():
+    case = CASES["noscale_k80"]
+    p = case["packed"].copy()
+    p[[0, 1]] = p[[1, 0]]  # swap two 16-deep k chunks of the prepack
+    out, _ = _run_case(case, packed=p)
+    assert not np.array_equal(out, case["out"])
+
+
+def test_compare_metric_flags_one_ulp_and_masks():
+    ref = oracle.f32_to_bf16(np.array([3.0, 1.0, 0.5, -2.5], np.float32))
+    out = ref.copy()
+    out[0] += 1  # one bf16 ulp at 3.0 = 2^-6
+    res = oracle.compare(out, ref, oracle.BF16, k=64)
+    assert res["n_over"] == 1 and res["n_over_one_ulp"] == 1 and not res["strict_ok"]
+    out2 = ref.copy()
+    out2[1] = 0x7FC0  # NaN where the reference is finite
+    assert not oracle.compare(out2, ref, oracle.BF16, k=64)["nan_ok"]

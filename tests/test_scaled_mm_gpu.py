@@ -1,0 +1,277 @@
+"""GPU parity of `scaled_mm_hip` against the CPU oracle (reference tests: tests/test_scaled_mm_hip.py).
+
+Same shapes, dtypes and tile sweep as the reference's tests (test_scaled_mm_hip.py:16-89), plus the
+BASELINE configurations, edge cases (NaN/inf, subnormals, bf16 past fp16's range, N % 16 == 8), the
+C ABI called directly, and determinism. Inputs are generated on the CPU with fixed seeds and copied to
+the GPU; the oracle evaluates every row for small shapes and a fixed row sample for large ones.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import bits_of, check_against_oracle, sample_rows, to_dev_bits
+from oracle import naive as oracle
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 0.01
+ATOL = {torch.float16: 2.0, torch.bfloat16: 16.0}
+
+SHAPES = [  # (M, N, K), reference test_scaled_mm_hip.py:16-27
+    (1, 128, 128),
+    (17, 96, 64),
+    (128, 128, 128),
+    (256, 256, 256),
+    (512, 1024, 5120),
+    (4111, 512, 256),
+    (4112, 1152, 1152),
+    (4304, 4304, 1152),
+    (5376, 512, 3072),
+    (2048, 1024, 5120),
+]
+TAIL_SHAPE = (67, 272, 304)
+DTYPES = [(torch.float8_e5m2, torch.float16), (torch.float8_e5m2, torch.bfloat16),
+          (torch.float8_e4m3fn, torch.bfloat16)]
+
+
+@pytest.fixture(scope="module")
+def fo():
+    import feather_ops
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return feather_ops
+
+
+def _tensor(shape, dtype, seed=0):
+    """The reference's `_tensor` (randn -> dtype), drawn on the CPU so the oracle sees the same bits."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype).cuda()
+
+
+def _ref_metric(out, a, b_prepacked, scale, bias, rows):
+    """The reference's own bound (relative Frobenius <= 1%, max-abs <= ATOL), on the oracle."""
+    from gpu_helpers import oracle_ref
+
+    ref = oracle.bits_to_f32(oracle_ref(a, b_prepacked, scale, bias, out.dtype, rows=rows),
+                             oracle.BF16 if out.dtype == torch.bfloat16 else oracle.F16).astype(np.float64)
+    got = out.float().cpu().numpy()[rows if rows is not None else slice(None)].astype(np.float64)
+    diff = np.abs(got - ref)
+    rel = np.linalg.norm(diff) / max(np.linalg.norm(ref), 1e-6)
+    return rel, diff.max()
+
+
+def _rows_for(M, N, K):
+    return None if M * N * K <= (1 << 27) else sample_rows(M)
+
+
+@pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b_dtype,out_dtype", DTYPES)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_shapes(fo, a_dtype, b_dtype, out_dtype, shape):
+    M, N, K = shape
+    a = _tensor((M, K), a_dtype)
+    b = _tensor((K, N), b_dtype, seed=1)
+    scale = torch.tensor(2.34, device="cuda", dtype=torch.float32)
+    bias = _tensor((N,), out_dtype, seed=2)
+    bp = fo.prepack_b_for_scaled_mm(b)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, out_dtype)
+    rows = _rows_for(M, N, K)
+    rel, max_abs = _ref_metric(out, a, bp, scale, bias, rows)
+    assert rel <= RTOL, f"rel={rel:.3g}"
+    assert max_abs <= ATOL[out_dtype], f"max_abs={max_abs:.3g}"
+    check_against_oracle(out, a, bp, scale, bias, rows=rows)
+
+
+def _all_tiles():
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    return SCALED_MM_TILES
+
+
+@pytest.mark.parametrize("tile", _all_tiles())
+def test_every_tile(fo, tile):
+    M, N, K = TAIL_SHAPE
+    a = _tensor((M, K), torch.float16)
+    b = _tensor((K, N), torch.float8_e5m2, seed=1)
+    scale = torch.tensor(0.75, device="cuda", dtype=torch.float32)
+    bias = _tensor((N,), torch.bfloat16, seed=2)
+    bp = fo.prepack_b_for_scaled_mm(b)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile)
+    check_against_oracle(out, a, bp, scale, bias)
+
+
+@pytest.mark.parametrize("tile", _all_tiles())
+def test_every_tile_bf16_in_fp16_out_n_mod_16_is_8(fo, tile):
+    M, N, K = 33, 200, 160
+    a = _tensor((M, K), torch.bfloat16)
+    b = _tensor((K, N), torch.float8_e5m2, seed=1)
+    bp = fo.prepack_b_for_scaled_mm(b)
+    out = fo.scaled_mm_hip(a, bp, torch.tensor(0.5, device="cuda"), None, torch.float16, tile=tile)
+    check_against_oracle(out, a, bp, torch.tensor(0.5), None)
+
+
+def test_scale_and_bias_are_optional(fo):
+    a = _tensor((96, 64), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((64, 128), torch.float8_e5m2, seed=1))
+    out = fo.scaled_mm_hip(a, bp, None, None, torch.float16)
+    check_against_oracle(out, a, bp, None, None)
+
+
+def test_heuristic_matches_a_measured_tile(fo):
+    a = _tensor((4112, 1152), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((1152, 1152), torch.float8_e5m2, seed=1))
+    scale = torch.tensor(1.5, device="cuda", dtype=torch.float32)
+    out = fo.scaled_mm_hip(a, bp, scale, None, torch.bfloat16)
+    check_against_oracle(out, a, bp, scale, None, rows=sample_rows(4112))
+
+
+# ---- BASELINE configurations (north-star recipe) -----------------------------------------------------------
+
+CONFIGS = {
+    "C1": (256, 1024, 1024, oracle.F16, False),
+    "C2": (4096, 3072, 3072, oracle.BF16, False),
+    "C3": (4096, 3072, 12288, oracle.F16, False),
+    "C4": (16, 4096, 14336, oracle.F16, False),
+    "C5_1_1000": (1, 2560, 1000, oracle.BF16, True),
+    "C5_77_5120": (77, 2560, 5120, oracle.BF16, True),
+    "C5_1000_1000": (1000, 2560, 1000, oracle.BF16, True),
+    "C5_4097_5120": (4097, 2560, 5120, oracle.BF16, True),
+}
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_baseline_config(fo, name):
+    m, k, n, a_fmt, outliers = CONFIGS[name]
+    a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, a_fmt, seed=0, outliers=outliers)
+    a = to_dev_bits(a_bits, torch.bfloat16 if a_fmt == oracle.BF16 else torch.float16, "cuda")
+    bp = to_dev_bits(packed, torch.float8_e5m2, "cuda")
+    s = torch.tensor(scale, dtype=torch.float32, device="cuda")
+    out_dtype = torch.bfloat16 if a_fmt == oracle.BF16 else torch.float16
+    out = fo.scaled_mm_hip(a, bp, s, None, out_dtype)
+    rows = None if m * n * k <= (1 << 28) else sample_rows(m, n_random=16)
+    res = check_against_oracle(out, a, bp, s, None, rows=rows)
+    print(f"{name}: max_abs={res['max_abs']:.4g} bound={res['bound']:.4g} over={res['n_over']} of {res['n']}")
+    # every output, against a torch fp32 reference of the same op on the GPU (upcast, fp32 matmul, scale)
+    b_dec = bp.permute(0, 2, 1).reshape(-1, n)[:k].to(torch.float32)
+    ref = ((a.to(torch.float16).float() @ b_dec) * s).to(out_dtype)
+    full = oracle.compare(bits_of(out), bits_of(ref), oracle.BF16 if out_dtype == torch.bfloat16 else oracle.F16, k)
+    assert full["nan_ok"] and full["inf_ok"]
+    assert full["n_over"] == full["n_over_one_ulp"] and full["n_over"] <= max(2, 1e-3 * full["n"]), full
+
+
+# ---- edge cases --------------------------------------------------------------------------------------------
+
+def test_specials_propagate_like_the_oracle(fo):
+    g = torch.Generator("cpu").manual_seed(9)
+    a = torch.randn(20, 64, generator=g).to(torch.float16)
+    a[3, 5] = float("inf")
+    a[7, 9] = float("nan")
+    codes = torch.randn(64, 24, generator=g).to(torch.float8_e5m2).view(torch.uint8)
+    codes[11, 4] = 0x7C  # +inf
+    codes[13, 17] = 0x7E  # NaN
+    bp = fo.prepack_b_for_scaled_mm(codes.view(torch.float8_e5m2).cuda())
+    for out_dtype in (torch.float16, torch.bfloat16):
+        out = fo.scaled_mm_hip(a.cuda(), bp, torch.tensor(0.5, device="cuda"), None, out_dtype)
+        check_against_oracle(out, a.cuda(), bp, torch.tensor(0.5), None)
+
+
+def test_bf16_activation_past_fp16_range_becomes_inf_like_naive(fo):
+    g = torch.Generator("cpu").manual_seed(10)
+    a = torch.randn(16, 32, generator=g).to(torch.bfloat16)
+    a[2, 0] = 70000.0  # fp16(70000) = inf under naive.py:21
+    bp = fo.prepack_b_for_scaled_mm(torch.randn(32, 16, generator=g).to(torch.float8_e5m2).cuda())
+    out = fo.scaled_mm_hip(a.cuda(), bp, None, None, torch.bfloat16)
+    assert not torch.isfinite(out[2]).any()
+    check_against_oracle(out, a.cuda(), bp, None, None)
+
+
+def test_subnormal_weights_and_activations(fo):
+    g = torch.Generator("cpu").manual_seed(11)
+    a = (torch.randn(32, 64, generator=g) * 1e-6).to(torch.float16)
+    codes = torch.randint(0, 4, (64, 32), generator=g, dtype=torch.uint8) | (
+        torch.randint(0, 2, (64, 32), generator=g, dtype=torch.uint8) << 7)
+    bp = fo.prepack_b_for_scaled_mm(codes.view(torch.float8_e5m2).cuda())
+    s = torch.tensor(2.0**20, device="cuda")
+    out = fo.scaled_mm_hip(a.cuda(), bp, s, None, torch.float16)
+    check_against_oracle(out, a.cuda(), bp, s.cpu(), None)
+
+
+def test_e4m3fn_all_codes(fo):
+    k = 256
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(k, 1).repeat(1, 16)
+    codes[codes & 0x7F == 0x7F] = 0x38  # NaN codes checked in test_specials; keep the sums finite here
+    a = torch.eye(k, dtype=torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(codes.view(torch.float8_e4m3fn).cuda())
+    out = fo.scaled_mm_hip(a.cuda(), bp, None, None, torch.float16)
+    check_against_oracle(out, a.cuda(), bp, None, None)
+
+
+def test_deterministic(fo):
+    a = _tensor((300, 512), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((512, 1000), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.01, device="cuda")
+    first = fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16)
+    for tile in [None, (4, 1, 4, 1, 4, 0)]:
+        x = fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16, tile=tile)
+        y = fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16, tile=tile)
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert torch.equal(first.view(torch.int16), fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16).view(torch.int16))
+
+
+def test_c_abi_direct(fo):
+    """launch_scaled_mm through ctypes on torch-owned device memory matches the torch op bit for bit."""
+    from feather_ops import _lib
+
+    lib = ctypes.CDLL(str(_lib.LIBRARY))
+    lib.launch_scaled_mm.restype = ctypes.c_bool
+    lib.launch_scaled_mm.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + \
+        [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_void_p]
+    M, N, K = 100, 256, 320
+    a = _tensor((M, K), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.3, device="cuda")
+    bias = _tensor((N,), torch.float16, seed=2)
+    want = fo.scaled_mm_hip(a, bp, s, bias, torch.float16, tile=(2, 2, 4, 4, 4, 1))
+    c = torch.empty_like(want)
+    ok = lib.launch_scaled_mm(a.data_ptr(), bp.data_ptr(), s.data_ptr(), bias.data_ptr(), c.data_ptr(), M, N, K, 1, 1,
+                              True, True, False, 2, 2, 4, 4, 4, True, torch.cuda.current_stream().cuda_stream)
+    assert ok
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), want.view(torch.int16))
+    # an uninstantiated tile is refused and enqueues nothing
+    assert not lib.launch_scaled_mm(a.data_ptr(), bp.data_ptr(), s.data_ptr(), bias.data_ptr(), c.data_ptr(), M, N, K,
+                                    1, 1, True, True, False, 3, 3, 3, 3, 3, True,
+                                    torch.cuda.current_stream().cuda_stream)
+
+
+def test_op_rejects_bad_inputs(fo):
+    a = _tensor((16, 64), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((64, 32), torch.float8_e5m2, seed=1))
+    with pytest.raises(RuntimeError, match="Unsupported config"):
+        fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=(3, 3, 3, 3, 3, 1))
+    with pytest.raises(RuntimeError, match="K must be divisible by 16"):
+        fo.scaled_mm_hip(a[:, :40], bp, None, None, torch.float16)
+    with pytest.raises(RuntimeError, match="scale must be float32"):
+        fo.scaled_mm_hip(a, bp, torch.tensor(1.0, device="cuda", dtype=torch.float16), None, torch.float16)
+    with pytest.raises(RuntimeError, match="bias must have the same dtype as c"):
+        fo.scaled_mm_hip(a, bp, None, torch.zeros(32, device="cuda", dtype=torch.bfloat16), torch.float16)
+
+
+def test_compile_matches_eager(fo):
+    """Reference tests/test_scaled_mm_hip_compile.py: one opaque node, eager == compiled."""
+    for dynamic in (False, True):
+        a = _tensor((512, 5120), torch.bfloat16)
+        bp = fo.prepack_b_for_scaled_mm(_tensor((5120, 1024), torch.float8_e5m2, seed=1))
+        s = torch.tensor(2.34, device="cuda")
+        bias = _tensor((1024,), torch.bfloat16, seed=2)
+
+        def run(a, bp, s, bias):
+            return fo.scaled_mm_hip(a, bp, s, bias, torch.bfloat16)
+
+        eager = run(a, bp, s, bias)
+        compiled = torch.compile(run, fullgraph=True, dynamic=dynamic)(a, bp, s, bias)
+        assert torch.equal(compiled.view(torch.int16), eager.view(torch.int16))
