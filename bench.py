@@ -1,0 +1,242 @@
+"""Benchmark of the fp16/bf16 x fp8e5m2 scaled matmul on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+
+Headline workload (BASELINE.json metric): C3, the DiT MLP up-projection, A fp16 [4096, 3072] x W e5m2
+[12288, 3072] (prepacked [192, 12288, 16], per-tensor scale) -> fp16 [4096, 12288]. One step is one
+`scaled_mm_hip` call on inputs already resident in HBM; K steps are timed with HIP events on the stream
+the kernels run on, bracketed by device synchronisation. value = TFLOP/s = 2*M*N*K / time per step.
+
+Also reported: the skinny HBM-bound cell C4 (A fp16 [16, 4096] x W e5m2 [14336, 4096]) as GB/s of
+algorithmic bytes, timed over a HIP graph of launches that rotate over 8 distinct weight copies (8 x
+58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), and the CPU oracle
+(oracle/scaled_mm_oracle.c, all host cores) on a row sample of C3 as `cpu_baseline`.
+
+Prints one JSON line (the driver's contract) on rank 0.
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "feather-ops_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+
+# HBM bytes per launch of the C3 kernel, by tile: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of
+# `bench.py --only c3` (KiB per dispatch), scaled by the factors a 512 MiB device-to-device copy gives the
+# same counters (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile
+# without a measurement reports null.
+MEASURED_TRAFFIC_BYTES = {
+    (2, 4, 4, 8, 4, 1): (147586 * 2.0 + 184295 * 1.0) * 1024,
+}
+
+
+def algorithmic_bytes(m: int, k: int, n: int, bias: bool = False) -> int:
+    """Each byte once: A (2MK) + prepacked weight (K_pad*N) + output (2MN) + scale (4) [+ bias (2N)]."""
+    k_pad = -(-k // 128) * 128
+    return 2 * m * k + k_pad * n + 2 * m * n + 4 + (2 * n if bias else 0)
+
+
+def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0):
+    import numpy as np
+    import torch
+
+    from oracle import naive as oracle  # the seeded input recipe (no oracle arithmetic on this path)
+
+    a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, a_fmt, seed=seed)
+    a_dtype = torch.bfloat16 if a_fmt == oracle.BF16 else torch.float16
+    a = torch.from_numpy(a_bits.view(np.int16)).view(a_dtype).cuda()
+    b0 = torch.from_numpy(packed).view(torch.float8_e5m2).cuda()
+    bs = [b0] + [b0.clone() for _ in range(copies - 1)]
+    s = torch.tensor(scale, dtype=torch.float32, device="cuda")
+    return a, bs, s, (a_bits, packed, scale)
+
+
+def time_c3(steps: int, warmup: int):
+    import torch
+
+    import feather_ops
+
+    m, k, n = 4096, 3072, 12288
+    a, bs, s, _ = make_device_inputs(m, k, n, "fp16")
+    b = bs[0]
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, b.dtype, torch.float16)
+    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    op = torch.ops.feather_ops.scaled_mm.default
+    for _ in range(warmup):
+        feather_ops.scaled_mm_hip(a, b, s, None, torch.float16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        op(a, b, s, None, out, *tile)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop) / steps
+    flops = 2.0 * m * n * k
+    return {"m": m, "k": k, "n": n, "tile": list(tile), "ms": ms, "wall_s": wall, "tflops": flops / (ms * 1e-3) / 1e12,
+            "bytes": algorithmic_bytes(m, k, n)}
+
+
+def time_c4(reps: int = 50, copies: int = 8):
+    import torch
+
+    import feather_ops
+
+    m, k, n = 16, 4096, 14336
+    a, bs, s, _ = make_device_inputs(m, k, n, "fp16", copies=copies)
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    outs = [torch.empty((m, n), dtype=torch.float16, device="cuda") for _ in range(copies)]
+    op = torch.ops.feather_ops.scaled_mm.default
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(copies):
+            op(a, bs[i], s, None, outs[i], *tile)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    launches = copies * 4
+    with torch.cuda.graph(graph):
+        for i in range(launches):
+            op(a, bs[i % copies], s, None, outs[i % copies], *tile)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / (reps * launches)
+    nbytes = algorithmic_bytes(m, k, n)
+    return {"m": m, "k": k, "n": n, "tile": list(tile), "us": us, "gbps": nbytes / (us * 1e-6) / 1e9,
+            "bytes": nbytes, "weight_copies": copies}
+
+
+def run_only(which: str, steps: int, warmup: int) -> None:
+    """One kernel, `warmup + steps` eager launches, nothing else: the target of rocprofv3 --pmc runs.
+
+    c3 / c4: the scaled_mm kernel on that cell (c4 rotates over 8 weight copies); copy: torch's
+    device-to-device copy of a 512 MiB buffer, whose FETCH_SIZE / WRITE_SIZE calibrate the counters
+    (1 x 512 MiB read and 1 x 512 MiB written per launch).
+    """
+    import torch
+
+    import feather_ops
+
+    if which == "copy":
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(warmup + steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
+    m, k, n, copies = (4096, 3072, 12288, 1) if which == "c3" else (16, 4096, 14336, 8)
+    a, bs, s, _ = make_device_inputs(m, k, n, "fp16", copies=copies)
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    op = torch.ops.feather_ops.scaled_mm.default
+    for i in range(warmup + steps):
+        op(a, bs[i % copies], s, None, out, *tile)
+    torch.cuda.synchronize()
+
+
+def time_cpu_oracle(budget_s: float = 10.0):
+    """The oracle on host cores over a row sample of C3, scaled to TFLOP/s of the same workload."""
+    import numpy as np
+
+    from oracle import naive as oracle
+
+    m, k, n = 4096, 3072, 12288
+    a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, oracle.F16, seed=0)
+    threads = min(16, oracle.cpu_count())
+    rows = 32
+    t0 = time.perf_counter()
+    oracle.scaled_mm(a_bits, oracle.F16, packed, oracle.E5M2, scale, None, oracle.F16,
+                     rows=np.arange(rows), threads=threads)
+    t_probe = time.perf_counter() - t0
+    rows = int(max(32, min(m, rows * budget_s / max(t_probe, 1e-3))))
+    sample = np.linspace(0, m - 1, rows).astype(np.int64)
+    t0 = time.perf_counter()
+    oracle.scaled_mm(a_bits, oracle.F16, packed, oracle.E5M2, scale, None, oracle.F16, rows=sample, threads=threads)
+    t = time.perf_counter() - t0
+    try:
+        model = next(line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo") if line.startswith("model name"))
+    except (OSError, StopIteration):
+        model = "unknown"
+    return {"value": 2.0 * rows * n * k / t / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"C3 rows: {rows} of {m} evenly spaced (x all {n} columns, K={k}), {t:.1f} s on {model}"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 HBM measurement")
+    parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (one GPU's share of the GEMM is "
+              "the kernel at its shard's shape); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    if args.only:
+        run_only(args.only, args.steps, args.warmup)
+        print(f"ran {args.only}: {args.warmup} + {args.steps} launches")
+        return 0
+    c3 = time_c3(args.steps, args.warmup)
+    c4 = None if args.no_secondary else time_c4()
+    cpu = None if args.no_cpu else time_cpu_oracle()
+
+    line = {
+        "metric": "TFLOP/s (% fp16 MFMA peak) at 4096x3072x12288; HBM GB/s at M=16",
+        "value": round(c3["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c3["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to e5m2 with a per-tensor scale)",
+        "config": {"workload": "C3 DiT MLP up-projection: fp16 [4096,3072] x e5m2 [12288,3072] -> fp16, scale, no bias",
+                   "M": c3["m"], "K": c3["k"], "N": c3["n"], "tile": c3["tile"],
+                   "pct_fp16_peak": round(100 * c3["tflops"] / PEAK_FP16_TFLOPS, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(c3["tflops"] / PEAK_FP16_TFLOPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(tuple(c3["tile"]))},
+    }
+    if c4 is not None:
+        line["hbm_cell"] = {"workload": "C4 skinny: fp16 [16,4096] x e5m2 [14336,4096] -> fp16",
+                            "GBps": round(c4["gbps"], 1), "us_per_launch": round(c4["us"], 3),
+                            "frac_hbm_peak": round(c4["gbps"] / PEAK_HBM_GBPS, 4), "tile": c4["tile"],
+                            "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"]}
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
