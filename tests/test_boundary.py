@@ -1,0 +1,107 @@
+"""The C ABI and torch-op boundary, checked without a GPU.
+
+The library must load and export every function include/feather_ops.h declares, refuse out-of-contract
+calls before touching the device (it returns false and enqueues nothing), and the torch ops must not
+accept CPU tensors (they are registered for the CUDA/HIP key only: no CPU fallback).
+"""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "feather_ops.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*bool\s+(\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from feather_ops import _lib
+
+    handle = ctypes.CDLL(str(_lib.LIBRARY))
+    handle.launch_scaled_mm.restype = ctypes.c_bool
+    handle.launch_scaled_mm.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + \
+        [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_void_p]
+    handle.feather_bf16_to_fp16.restype = ctypes.c_bool
+    handle.feather_bf16_to_fp16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    return handle
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16"}
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+# Fake, 16-byte aligned device addresses: every call below is refused before anything dereferences them.
+A, B, S, BIAS, C = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+GOOD = dict(M=64, N=128, K=256)
+TILE = (2, 2, 4, 4, 4, True)
+
+
+def _call(lib, a=A, b=B, s=S, bias=BIAS, c=C, M=64, N=128, K=256, has_scale=1, has_bias=1, tile=TILE):
+    return lib.launch_scaled_mm(a, b, s, bias, c, M, N, K, has_scale, has_bias, True, False, False, *tile, None)
+
+
+@pytest.mark.parametrize("kwargs", [
+    dict(tile=(3, 3, 3, 3, 3, True)),          # not instantiated (the reference's only false case)
+    dict(tile=(2, 2, 4, 4, 4, False)),         # right numbers, wrong kernel family
+    dict(N=100),                               # N % 8 != 0
+    dict(K=40),                                # K % 16 != 0
+    dict(K=0),
+    dict(M=0),
+    dict(a=A + 8),                             # misaligned
+    dict(c=C + 2),
+    dict(bias=BIAS + 2),
+    dict(has_scale=1, s=None),
+    dict(a=None),
+    dict(M=1 << 20, K=1 << 11),                # a would be 4 GiB
+])
+def test_c_abi_refuses_out_of_contract_calls(lib, kwargs):
+    assert _call(lib, **kwargs) is False
+
+
+def test_convert_c_abi_refuses_bad_arguments(lib):
+    assert lib.feather_bf16_to_fp16(A, C, -1, None) is False
+    assert lib.feather_bf16_to_fp16(A + 2, C, 16, None) is False
+    assert lib.feather_bf16_to_fp16(None, C, 16, None) is False
+    assert lib.feather_bf16_to_fp16(A, C, 0, None) is True  # nothing to do, nothing enqueued
+
+
+def test_torch_ops_are_registered_for_the_gpu_only():
+    import feather_ops  # noqa: F401
+
+    a = torch.zeros(16, 64, dtype=torch.float16)
+    b = torch.zeros(8, 32, 16, dtype=torch.float8_e5m2)
+    c = torch.empty(16, 32, dtype=torch.float16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.feather_ops.scaled_mm.default(a, b, None, None, c, 2, 2, 4, 4, 4, True)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.feather_ops.bf16_to_fp16.default(torch.zeros(8, dtype=torch.bfloat16), torch.empty(8, dtype=torch.float16))
+
+
+def test_scaled_mm_hip_has_no_cpu_fallback():
+    from feather_ops import scaled_mm_hip
+
+    a = torch.zeros(16, 64, dtype=torch.float16)
+    b = torch.zeros(8, 32, 16, dtype=torch.float8_e5m2)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        scaled_mm_hip(a, b, None, None, torch.float16)
+
+
+def test_heuristic_returns_instantiated_tiles():
+    from feather_ops.scaled_mm import select_scaled_mm_config
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    for m in (1, 2, 15, 16, 17, 31, 32, 33, 64, 65, 77, 128, 256, 500, 1000, 4096, 4097, 25344):
+        for n in (8, 96, 1000, 1024, 3072, 5120, 12288, 14336, 96768):
+            for k in (16, 1024, 2560, 4096):
+                assert select_scaled_mm_config(m, n, k) in SCALED_MM_TILES

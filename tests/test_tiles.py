@@ -1,0 +1,53 @@
+"""The tile table (reference tests/test_tiles.py): header current, heuristic aliases instantiated, no
+duplicates, and every tile fits gfx950's limits."""
+
+import pathlib
+import subprocess
+import sys
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def test_generated_header_is_current():
+    result = subprocess.run([sys.executable, str(ROOT / "feather-ops_amd" / "gen_tiles.py"), "--check"],
+                            capture_output=True, text=True, check=False)
+    assert result.returncode == 0, f"{result.stdout}{result.stderr}"
+
+
+def test_heuristic_tiles_are_instantiated():
+    from feather_ops import scaled_mm
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    aliases = [name for name in dir(scaled_mm) if name.startswith("_TILE_")]
+    assert aliases
+    for name in aliases:
+        assert getattr(scaled_mm, name) in SCALED_MM_TILES, name
+
+
+def test_no_duplicate_tiles():
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    assert len(set(SCALED_MM_TILES)) == len(SCALED_MM_TILES)
+
+
+def test_tiles_fit_gfx950():
+    from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, threads_per_block
+
+    for tile in SCALED_MM_TILES:
+        wm, wn, u, rm, rn, pf = tile
+        assert pf in (0, 1)
+        assert u % 4 == 0, tile  # whole 64-deep MFMA groups
+        assert threads_per_block(tile) <= 1024, tile
+        bm, bn, ck = gemm_block_sizes(tile)
+        if pf:
+            lds = 2 * (bm * ck * 2 + bn * ck)  # double-buffered A (fp16) + B (fp8) stages
+        else:
+            lds = (wm - 1) * wn * rm * rn * 64 * 16  # K-slice reduction buffer
+        assert lds <= 160 * 1024, tile
+
+
+def test_tile_shape_formula():
+    from feather_ops.scaled_mm import tile_shape
+
+    assert tile_shape((2, 4, 4, 8, 4, 1)) == (256, 256, 64)
+    assert tile_shape((4, 1, 4, 1, 4, 0)) == (16, 64, 64)  # stream tiles split K across warps_m
