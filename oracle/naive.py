@@ -22,6 +22,9 @@ What pins each function (tests/test_oracle.py):
   power-of-two scales), brute-force float64 loops on tiny inputs, and golden fixtures computed by float64
   `numpy.matmul` on the decoded operands (`tests/golden/make_golden.py`), chosen non-square and
   non-symmetric so that a transposed operand, a dropped k term or a wrong scale/bias order fails.
+- `scaled_mm_band`: the same core as `scaled_mm` evaluated at the fp32 value -/+ delta; pinned by the
+  answer at delta = 0 (itself pinned by the goldens) and by monotonicity (lo <= answer <= hi) on a
+  seeded bf16 cell.
 - `literal_fp16_scaled_mm`: the reference's fp16-accumulate form, pinned by the same closed forms; it is
   only used to show the overflow that rules it out as an oracle at BASELINE's quantization.
 """
@@ -74,6 +77,12 @@ def _load():
             ctypes.POINTER(ctypes.c_int64), i64, ctypes.c_int,
         ]
         lib.oracle_scaled_mm_f32.restype = None
+        lib.oracle_scaled_mm_band.argtypes = [
+            u16p, ctypes.c_int, u8p, ctypes.c_int, i64, i64, i64,
+            ctypes.POINTER(ctypes.c_float), u16p, ctypes.c_int, ctypes.c_float, u16p, u16p,
+            ctypes.POINTER(ctypes.c_int64), i64, ctypes.c_int,
+        ]
+        lib.oracle_scaled_mm_band.restype = None
         lib.oracle_prepack.argtypes = [u8p, i64, i64, u8p]
         lib.oracle_prepack.restype = None
         for name in ("oracle_e5m2_to_f32", "oracle_e4m3fn_to_f32"):
@@ -203,6 +212,35 @@ def scaled_mm_f32(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str
         None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),
     )
     return out
+
+
+def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale: float | None,
+                   bias_bits: np.ndarray | None, out_fmt: str, delta: float, rows: np.ndarray | None = None,
+                   threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """The oracle's answers had the fp32 pre-rounding value been `delta` lower / higher (output units).
+
+    An implementation whose fp32 sum differs from the exact one only in summation order produces, for
+    every element, the oracle's answer at some value within a small band around the exact one; an output
+    that equals neither the answer nor the band's ends is an error, not a rounding-neighbour flip.
+    """
+    a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    m, k = a_bits.shape
+    _, n, _ = packed.shape
+    sc = None if scale is None else np.array([scale], dtype=np.float32)
+    bias = None if bias_bits is None else np.ascontiguousarray(bias_bits, dtype=np.uint16)
+    rws = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    r = m if rws is None else len(rws)
+    lo = np.empty((r, n), dtype=np.uint16)
+    hi = np.empty((r, n), dtype=np.uint16)
+    _load().oracle_scaled_mm_band(
+        _ptr(a_bits, ctypes.c_uint16), int(a_fmt == BF16), _ptr(packed, ctypes.c_uint8), int(b_fmt == E5M2),
+        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float),
+        None if bias is None else _ptr(bias, ctypes.c_uint16), int(out_fmt == BF16), float(delta),
+        _ptr(lo, ctypes.c_uint16), _ptr(hi, ctypes.c_uint16),
+        None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),
+    )
+    return lo, hi
 
 
 def literal_fp16_scaled_mm(a_f16: np.ndarray, b_f16: np.ndarray, scale: float | None) -> np.ndarray:

@@ -140,20 +140,40 @@ uint16_t oracle_f32_to_bf16_rne(float f) {
     return (uint16_t)(wide >> 16);
 }
 
+static uint16_t finish(float y, const uint16_t* bias, int64_t n, int out_bf16) {
+    uint16_t o;
+    if (out_bf16) {
+        o = oracle_f32_to_bf16_rne(y);
+        if (bias) {
+            o = oracle_f32_to_bf16_rne(oracle_bf16_to_f32(o) + oracle_bf16_to_f32(bias[n]));
+        }
+    } else {
+        o = oracle_f32_to_f16_rne(y);
+        if (bias) {
+            o = oracle_f32_to_f16_rne(oracle_f16_to_f32(o) + oracle_f16_to_f32(bias[n]));
+        }
+    }
+    return o;
+}
+
 /*
- * out[m, n] = round_out( fp32(sum_k widen(a[m, k]) * decode(B[k, n])) * scale ) (+ bias[n], in out precision)
- * with B read from the prepack: B[k, n] = packed[(k / 16) * N * 16 + n * 16 + (k % 16)]
- * (feather_ops/scaled_mm.py:150, feather_ops/naive.py:15-16).
+ * The shared core: y[r, n] = fp32(exact sum_k widen(a[m, k]) * decode(B[k, n])) (* scale, in fp32), with B
+ * read from the prepack: B[k, n] = packed[(k / 16) * N * 16 + n * 16 + (k % 16)] (feather_ops/scaled_mm.py:150,
+ * feather_ops/naive.py:15-16). Then, per mode:
+ *   out      != NULL: out[r, n]  = finish(y)                        (the oracle's answer)
+ *   out_f32  != NULL: out_f32[r, n] = y                             (diagnostics)
+ *   lo, hi   != NULL: lo/hi[r, n] = finish(y -/+ delta)             (the answers for a sum off by +-delta)
+ * finish() rounds to the output dtype (RNE) and adds the bias in output precision (naive.py:34-40).
  *
  * a_bf16:  a holds bf16 bits, widened to fp16 with RNE first (naive.py:21 a.to(fp16)); else fp16 bits.
  * b_e5m2:  packed holds e5m2 codes; else e4m3fn codes.
  * scale:   one fp32 value or NULL (no scale step: naive.py:24 skipped).
  * bias:    N values in the output dtype or NULL.
- * rows:    optional list of n_rows row indices to compute (NULL = all M rows); out is then [n_rows, N].
+ * rows:    optional list of n_rows row indices to compute (NULL = all M rows); outputs are [n_rows, N].
  */
-void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
-                      int64_t K, const float* scale, const uint16_t* bias, int out_bf16, uint16_t* out,
-                      const int64_t* rows, int64_t n_rows, int n_threads) {
+static void core(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N, int64_t K,
+                 const float* scale, const uint16_t* bias, int out_bf16, uint16_t* out, float* out_f32, float delta,
+                 uint16_t* lo, uint16_t* hi, const int64_t* rows, int64_t n_rows, int n_threads) {
     const int64_t R = rows ? n_rows : M;
     float lut[256];
     for (int c = 0; c < 256; ++c) {
@@ -169,7 +189,6 @@ void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int 
             bcol[n * K + k] = lut[packed[((k / 16) * N + n) * 16 + (k % 16)]];
         }
     }
-    const float s = scale ? *scale : 1.0f;
 #ifdef _OPENMP
     if (n_threads > 0) {
         omp_set_num_threads(n_threads);
@@ -196,21 +215,20 @@ void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int 
                 }
                 float y = (float)acc;
                 if (scale) {
-                    y = y * s;
+                    y = y * *scale;
                 }
-                uint16_t o;
-                if (out_bf16) {
-                    o = oracle_f32_to_bf16_rne(y);
-                    if (bias) {
-                        o = oracle_f32_to_bf16_rne(oracle_bf16_to_f32(o) + oracle_bf16_to_f32(bias[n]));
-                    }
-                } else {
-                    o = oracle_f32_to_f16_rne(y);
-                    if (bias) {
-                        o = oracle_f32_to_f16_rne(oracle_f16_to_f32(o) + oracle_f16_to_f32(bias[n]));
-                    }
+                if (out) {
+                    out[r * N + n] = finish(y, bias, n, out_bf16);
                 }
-                out[r * N + n] = o;
+                if (out_f32) {
+                    out_f32[r * N + n] = y;
+                }
+                if (lo) {
+                    lo[r * N + n] = finish((float)((double)y - (double)delta), bias, n, out_bf16);
+                }
+                if (hi) {
+                    hi[r * N + n] = finish((float)((double)y + (double)delta), bias, n, out_bf16);
+                }
             }
         }
         free(arow_f);
@@ -218,55 +236,26 @@ void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int 
     free(bcol);
 }
 
-/* The fp32 value before the output rounding, for diagnostics: acc32[r, n] = fp32(sum) (* scale). */
+void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
+                      int64_t K, const float* scale, const uint16_t* bias, int out_bf16, uint16_t* out,
+                      const int64_t* rows, int64_t n_rows, int n_threads) {
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, bias, out_bf16, out, NULL, 0.0f, NULL, NULL, rows, n_rows,
+         n_threads);
+}
+
+/* The fp32 value before the output rounding, for diagnostics: out[r, n] = fp32(sum) (* scale). */
 void oracle_scaled_mm_f32(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
                           int64_t K, const float* scale, float* out, const int64_t* rows, int64_t n_rows,
                           int n_threads) {
-    const int64_t R = rows ? n_rows : M;
-    float lut[256];
-    for (int c = 0; c < 256; ++c) {
-        lut[c] = b_e5m2 ? oracle_e5m2_to_f32((uint8_t)c) : oracle_e4m3fn_to_f32((uint8_t)c);
-    }
-    float* bcol = (float*)malloc((size_t)N * (size_t)K * sizeof(float));
-    if (!bcol) {
-        return;
-    }
-    for (int64_t n = 0; n < N; ++n) {
-        for (int64_t k = 0; k < K; ++k) {
-            bcol[n * K + k] = lut[packed[((k / 16) * N + n) * 16 + (k % 16)]];
-        }
-    }
-#ifdef _OPENMP
-    if (n_threads > 0) {
-        omp_set_num_threads(n_threads);
-    }
-#pragma omp parallel
-#endif
-    {
-        double* arow_f = (double*)malloc((size_t)K * sizeof(double));
-#ifdef _OPENMP
-#pragma omp for schedule(dynamic, 1)
-#endif
-        for (int64_t r = 0; r < R; ++r) {
-            const int64_t m = rows ? rows[r] : r;
-            for (int64_t k = 0; k < K; ++k) {
-                const uint16_t v = a[m * K + k];
-                arow_f[k] = a_bf16 ? oracle_f16_to_f32(oracle_f32_to_f16_rne(oracle_bf16_to_f32(v)))
-                                   : oracle_f16_to_f32(v);
-            }
-            for (int64_t n = 0; n < N; ++n) {
-                const float* bc = bcol + n * K;
-                double acc = 0.0;
-                for (int64_t k = 0; k < K; ++k) {
-                    acc += arow_f[k] * (double)bc[k];
-                }
-                float y = (float)acc;
-                out[r * N + n] = scale ? y * *scale : y;
-            }
-        }
-        free(arow_f);
-    }
-    free(bcol);
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, NULL, 0, NULL, out, 0.0f, NULL, NULL, rows, n_rows, n_threads);
+}
+
+/* The answers for a pre-rounding value off by -delta / +delta (absolute, output units). */
+void oracle_scaled_mm_band(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
+                           int64_t K, const float* scale, const uint16_t* bias, int out_bf16, float delta,
+                           uint16_t* lo, uint16_t* hi, const int64_t* rows, int64_t n_rows, int n_threads) {
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, bias, out_bf16, NULL, NULL, delta, lo, hi, rows, n_rows,
+         n_threads);
 }
 
 /* [K, N] fp8 codes -> (K_pad/16, N, 16) with K zero-padded to a multiple of 128 (scaled_mm.py:137-150). */

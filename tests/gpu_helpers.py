@@ -40,10 +40,18 @@ def oracle_ref(a: torch.Tensor, b_prepacked: torch.Tensor, scale, bias, out_dtyp
     )
 
 
+BAND_REL = 1e-4  # half-width of the accepted band around the exact sum, relative to RMS(reference)
+
+
 def check_against_oracle(out: torch.Tensor, a, b_prepacked, scale, bias, rows=None, max_flip_frac=1e-3):
-    """North-star comparison with the oracle: strict for fp16 output; for bf16 output the only excess
-    allowed is exact one-ulp rounding neighbours (fp32 summation order at a bf16 rounding midpoint), at
-    most `max_flip_frac` of the outputs. Returns the comparison dict."""
+    """North-star comparison with the oracle.
+
+    Strict (max|out - ref| <= 1e-2 sqrt(K)/64 RMS, identical NaN/Inf masks) for fp16 output. For bf16
+    output the bound is below one bf16 ulp at |y| >= 2 RMS, so an element over it is accepted only when
+    it is exactly the oracle's answer for a pre-rounding value within BAND_REL * RMS of the exact sum
+    (an fp32 summation-order flip at a rounding midpoint, possibly carried through the bias add), and such
+    elements must be at most `max_flip_frac` of the outputs. Returns the comparison dict.
+    """
     fmt = FMT_OF[out.dtype]
     ref = oracle_ref(a, b_prepacked, scale, bias, out.dtype, rows=rows)
     got = bits_of(out)
@@ -51,9 +59,20 @@ def check_against_oracle(out: torch.Tensor, a, b_prepacked, scale, bias, rows=No
         got = got[rows]
     res = oracle.compare(got, ref, fmt, a.shape[1])
     assert res["nan_ok"] and res["inf_ok"], res
-    if fmt == oracle.F16:
+    if fmt == oracle.F16 or res["strict_ok"]:
         assert res["strict_ok"], res
-    else:
-        assert res["n_over"] == res["n_over_one_ulp"], res
-        assert res["n_over"] <= max(2, max_flip_frac * res["n"]), res
+        return res
+    lo, hi = oracle.scaled_mm_band(
+        bits_of(a), FMT_OF[a.dtype], bits_of(b_prepacked), FMT_OF[b_prepacked.dtype],
+        None if scale is None else float(scale.item()), None if bias is None else bits_of(bias), fmt,
+        BAND_REL * res["rms"], rows=rows, threads=16)
+    got_f = oracle.bits_to_f32(got, fmt).astype(np.float64)
+    ref_f = oracle.bits_to_f32(ref, fmt).astype(np.float64)
+    over = np.abs(got_f - ref_f) > res["bound"]
+    over &= np.isfinite(got_f) & np.isfinite(ref_f)
+    in_band = (got == lo) | (got == hi)
+    bad = over & ~in_band
+    assert not bad.any(), {**res, "n_outside_band": int(bad.sum())}
+    assert over.sum() <= max(2, max_flip_frac * res["n"]), res
+    res["n_band_flips"] = int(over.sum())
     return res

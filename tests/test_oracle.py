@@ -307,3 +307,13 @@ def test_compare_metric_flags_one_ulp_and_masks():
     out2 = ref.copy()
     out2[1] = 0x7FC0  # NaN where the reference is finite
     assert not oracle.compare(out2, ref, oracle.BF16, k=64)["nan_ok"]
+
+
+def test_band_brackets_the_answer_and_collapses_at_zero():
+    a_bits, packed, scale, _ = oracle.make_inputs(32, 512, 256, oracle.BF16, seed=3)
+    ref = oracle.scaled_mm(a_bits, oracle.BF16, packed, oracle.E5M2, scale, None, oracle.BF16)
+    lo0, hi0 = oracle.scaled_mm_band(a_bits, oracle.BF16, packed, oracle.E5M2, scale, None, oracle.BF16, 0.0)
+    assert np.array_equal(lo0, ref) and np.array_equal(hi0, ref)
+    lo, hi = oracle.scaled_mm_band(a_bits, oracle.BF16, packed, oracle.E5M2, scale, None, oracle.BF16, 0.05)
+    f = lambda x: oracle.bits_to_f32(x, oracle.BF16)  # noqa: E731
+    assert (f(lo) <= f(ref)).all() and (f(ref) <= f(hi)).all() and (f(lo) < f(hi)).any()
