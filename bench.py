@@ -125,7 +125,7 @@ def time_c4(reps: int = 50, copies: int = 8):
             "bytes": nbytes, "weight_copies": copies}
 
 
-def run_only(which: str, steps: int, warmup: int) -> None:
+def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     """One kernel, `warmup + steps` eager launches, nothing else: the target of rocprofv3 --pmc runs.
 
     c3 / c4: the scaled_mm kernel on that cell (c4 rotates over 8 weight copies); copy: torch's
@@ -145,7 +145,8 @@ def run_only(which: str, steps: int, warmup: int) -> None:
         return
     m, k, n, copies = (4096, 3072, 12288, 1) if which == "c3" else (16, 4096, 14336, 8)
     a, bs, s, _ = make_device_inputs(m, k, n, "fp16", copies=copies)
-    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    if tile is None:
+        tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
     op = torch.ops.feather_ops.scaled_mm.default
     for i in range(warmup + steps):
@@ -188,6 +189,7 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     parser.add_argument("--no-secondary", action="store_true", help="skip the C4 HBM measurement")
     parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
+    parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one GPU's share of the GEMM is "
@@ -200,7 +202,8 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     if args.only:
-        run_only(args.only, args.steps, args.warmup)
+        tile = tuple(int(v) for v in args.tile.split(",")) if args.tile else None
+        run_only(args.only, args.steps, args.warmup, tile)
         print(f"ran {args.only}: {args.warmup} + {args.steps} launches")
         return 0
     c3 = time_c3(args.steps, args.warmup)

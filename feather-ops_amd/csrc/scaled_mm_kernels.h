@@ -411,6 +411,449 @@ __global__ __launch_bounds__(kWave * WM * WN) void ring_kernel(const Params p) {
     store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
 }
 
+// ---- ring kernel with direct-to-LDS loads (fp16 activations) -------------------------------------------------
+
+// s_waitcnt immediate that waits until at most n vector-memory operations of this wave are outstanding
+// and leaves the other counters alone (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+constexpr int vmcnt_imm(int n) {
+    return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8);
+}
+
+// Workgroup barrier that does not wait for outstanding loads (unlike __syncthreads, whose fence waits
+// for every in-flight load, including the ones filling later ring stages). The memory clobber keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier_only() {
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at lds_dst + 16 * lane (lds_dst is
+// wave-uniform). soff is a scalar (SGPR) offset, so a per-lane offset computed once can walk K.
+__device__ __forceinline__ void dma16(rsrc_t r, const uint8_t* lds_dst, uint32_t voff, uint32_t soff = 0) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(reinterpret_cast<uintptr_t>(lds_dst)), 16,
+        static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+}
+
+template <int WM, int WN, int U, int RM, int RN>
+struct DmaShape {
+    static constexpr int kWaves = WM * WN;
+    static constexpr int kThreads = kWave * kWaves;
+    static constexpr int kBM = 16 * WM * RM;
+    static constexpr int kBN = 16 * WN * RN;
+    static constexpr int kGroups = U / 4;
+    static constexpr int kUnitsPerRow = 2 * U;            // 16-byte units in one A row of a stage
+    static constexpr int kABytes = kBM * U * 32;          // A: [row][2U units], units XOR-swizzled per row
+    static constexpr int kBBytes = kBN * U * 16;          // B: [chunk][col][16 bytes]
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    // Blocks of up to 4 waves keep a 2-stage ring when that lets two blocks share a CU, so one block's
+    // MFMAs run while the other waits at its barrier; bigger blocks keep 3 stages in flight.
+    static constexpr int kStages = (kWaves <= 4 && 2 * kStageBytes <= 80 * 1024) ? 2 : 3;
+    static constexpr int kLdsBytes = kStages * kStageBytes;
+    // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two.
+    static constexpr int kWavesPerEu = (kStages == 2 ? 2 : 1) * ((kWaves + 3) / 4);
+    static constexpr int kAInstr = kBM * kUnitsPerRow / kWave / kWaves;   // 1 KiB direct loads per wave
+    static constexpr int kBInstr = U * kBN / kWave / kWaves;
+    static constexpr int kLoadsPerStage = kAInstr + kBInstr;
+    static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
+    static_assert(kBM * kUnitsPerRow % (kWave * kWaves) == 0, "A stage splits into whole wave loads");
+    static_assert(kBN % kWave == 0 && (U * kBN / kWave) % kWaves == 0, "B stage splits into whole wave loads");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+    static_assert(kLoadsPerStage < 64, "vmcnt range");
+};
+
+// Physical 16-byte unit of logical unit u in A row `row`. The XOR key depends on row mod 16 only, so it is
+// the same for every 16-row fragment a lane reads and folds into one per-lane base address. With 8
+// units per row (128-byte rows) the key (r ^ (r >> 3)) & 7 gives the 16 rows one fragment read touches
+// 16 distinct bank groups whether the LDS serves 8 or 16 lanes of a 16-byte read per cycle; wider rows
+// use r itself.
+template <int kUnits>
+__device__ __forceinline__ int a_swizzle_key(int row) {
+    const int r = row & 15;
+    if constexpr (kUnits == 8) {
+        return (r ^ (r >> 3)) & 7;
+    } else {
+        return r & (kUnits - 1);
+    }
+}
+
+template <int kUnits>
+__device__ __forceinline__ int a_unit_phys(int row, int u) {
+    return u ^ a_swizzle_key<kUnits>(row);
+}
+
+template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kOutBf16>
+__global__ __launch_bounds__(kWave * WM * WN)
+__attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) void ring_dma_kernel(const Params p) {
+    using S = DmaShape<WM, WN, U, RM, RN>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: scalar LDS addresses
+    const int wave_m = wave / WN;
+    const int wave_n = wave % WN;
+
+    const int tiles_m = (p.M + S::kBM - 1) / S::kBM;
+    const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * S::kBM;
+    const int n0 = tn * S::kBN;
+
+    const rsrc_t a_rsrc = make_rsrc(p.a, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.K) * 2u);
+    const rsrc_t b_rsrc = make_rsrc(p.b, static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u);
+    const int k_chunks = p.K / 16;
+    const int stages = (p.K + 16 * U - 1) / (16 * U);
+    const int full_stages = k_chunks / U;  // stages with every chunk inside K
+
+    // Direct loads: instruction i of this wave fills 1 KiB of LDS, lane l the l-th 16 bytes of it. The
+    // per-lane offsets are for stage 0; a stage adds a scalar offset. Out-of-range rows and columns carry
+    // kOob, which stays past the buffer's end whatever is added.
+    uint32_t a_off[S::kAInstr];
+    int a_chunk[S::kAInstr];
+#pragma unroll
+    for (int i = 0; i < S::kAInstr; ++i) {
+        const int unit = (wave + i * S::kWaves) * kWave + lane;
+        const int row = unit / S::kUnitsPerRow;
+        const int u = a_unit_phys<S::kUnitsPerRow>(row, unit % S::kUnitsPerRow);  // XOR is its own inverse
+        a_chunk[i] = u >> 1;
+        const int grow = m0 + row;
+        a_off[i] = grow < p.M ? (static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.K) +
+                                 static_cast<uint32_t>(u * 8)) * 2u
+                              : kOob;
+    }
+    uint32_t b_off[S::kBInstr];
+    int b_chunk[S::kBInstr];
+#pragma unroll
+    for (int i = 0; i < S::kBInstr; ++i) {
+        const int unit = (wave + i * S::kWaves) * kWave + lane;
+        const int chunk = unit / S::kBN;
+        const int gcol = n0 + unit % S::kBN;
+        b_chunk[i] = chunk;
+        b_off[i] = gcol < p.N ? (static_cast<uint32_t>(chunk) * static_cast<uint32_t>(p.N) +
+                                 static_cast<uint32_t>(gcol)) * 16u
+                              : kOob;
+    }
+    const uint32_t b_stage_stride = static_cast<uint32_t>(U) * static_cast<uint32_t>(p.N) * 16u;
+
+    auto issue = [&](int stage) {
+        uint8_t* base = lds + (stage % S::kStages) * S::kStageBytes;
+        const uint32_t a_soff = static_cast<uint32_t>(stage) * static_cast<uint32_t>(U) * 32u;
+        const uint32_t b_soff = static_cast<uint32_t>(stage) * b_stage_stride;
+        if (stage < full_stages) {
+#pragma unroll
+            for (int i = 0; i < S::kAInstr; ++i) dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, a_off[i], a_soff);
+#pragma unroll
+            for (int i = 0; i < S::kBInstr; ++i) {
+                dma16(b_rsrc, base + S::kABytes + (wave + i * S::kWaves) * 1024, b_off[i], b_soff);
+            }
+        } else {
+            // The ragged last stage: chunks past K read zeros.
+            const int chunk0 = stage * U;
+#pragma unroll
+            for (int i = 0; i < S::kAInstr; ++i) {
+                const bool ok = chunk0 + a_chunk[i] < k_chunks;
+                dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? a_off[i] : kOob, a_soff);
+            }
+#pragma unroll
+            for (int i = 0; i < S::kBInstr; ++i) {
+                const bool ok = chunk0 + b_chunk[i] < k_chunks;
+                dma16(b_rsrc, base + S::kABytes + (wave + i * S::kWaves) * 1024, ok ? b_off[i] : kOob, b_soff);
+            }
+        }
+    };
+
+    f32x4 acc[RM][RN];
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int g = lane >> 4;
+    const int r16 = lane & 15;
+    const int a_row_base = wave_m * 16 * RM + r16;
+    const int b_col_base = wave_n * 16 * RN + r16;
+
+    // Per-lane LDS byte offsets within a stage; everything else is a compile-time immediate. Lane group g
+    // reads chunk 4q + g of the stage, whose two 16-byte halves (s = 0, 1) sit at units (8q + 2g + s) ^ key
+    // of the row; the key depends on the lane only (row mod 16), so each (q, s) needs one base register.
+    const int key = a_swizzle_key<S::kUnitsPerRow>(a_row_base);
+    int a_lane[S::kGroups][2];
+#pragma unroll
+    for (int q = 0; q < S::kGroups; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+            a_lane[q][s2] = a_row_base * (S::kUnitsPerRow * 16) + (((8 * q + 2 * g + s2) ^ key) << 4);
+    const int b_lane = S::kABytes + g * S::kBN * 16 + b_col_base * 16;
+
+    auto compute = [&](const uint8_t* stage_base) {
+#pragma unroll
+        for (int q = 0; q < S::kGroups; ++q) {
+            u32x4 braw[RN];
+#pragma unroll
+            for (int j = 0; j < RN; ++j) {
+                braw[j] = *reinterpret_cast<const u32x4*>(stage_base + b_lane + (4 * q * S::kBN + 16 * j) * 16);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                half8 w[RN];
+#pragma unroll
+                for (int j = 0; j < RN; ++j) {
+                    half8 w0, w1;
+                    decode_chunk<kE5M2>(braw[j], w0, w1);
+                    w[j] = s == 0 ? w0 : w1;
+                }
+#pragma unroll
+                for (int i = 0; i < RM; ++i) {
+                    const half8 x = *reinterpret_cast<const half8*>(
+                        stage_base + a_lane[q][s] + i * 16 * S::kUnitsPerRow * 16);
+#pragma unroll
+                    for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
+                }
+            }
+        }
+    };
+
+    issue(0);
+    if (S::kStages == 3 && stages > 1) issue(1);
+
+    // One trip of the ring per outer iteration, so every stage's buffer is a compile-time offset.
+    for (int t0 = 0; t0 < stages; t0 += S::kStages) {
+#pragma unroll
+        for (int b = 0; b < S::kStages; ++b) {
+            const int t = t0 + b;
+            if (t < stages) {
+                // Stage t's loads are this wave's oldest; the barrier then makes every wave's share visible
+                // and retires all reads of the buffer the next issued stage reuses (it held stage t - 1).
+                if (S::kStages == 3 && t + 1 < stages) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerStage));
+                } else {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                }
+                barrier_only();
+                if (t + S::kStages - 1 < stages) issue(t + S::kStages - 1);
+                compute(lds + b * S::kStageBytes);
+            }
+        }
+    }
+
+    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
+}
+
+// ---- ping-pong ring kernel (fp16 activations, 8 waves) ----------------------------------------------------
+//
+// A vector-memory instruction in the instruction stream of a wave that is issuing MFMAs costs that wave
+// about as much issue time as an MFMA, while the same instruction from another wave on the SIMD does not
+// slow the MFMAs down. So the 8 waves split into two groups of 4 (waves 0-3 and 4-7, one of each per
+// SIMD) that alternate every phase: one group runs a pure compute phase (decode + 64 MFMAs on fragments
+// already in registers) while the other runs a memory phase (its share of the direct global->LDS refill
+// and the LDS->register reads of its next 64-deep step). A workgroup barrier separates phases; group B
+// runs one phase behind group A, so the MFMA pipe of every SIMD always has a compute wave.
+//
+// Block tile BM x BN (WM x WN waves, WM even): group A owns rows [0, BM/2), group B rows [BM/2, BM).
+// K steps of 64 go through a 3-buffer LDS ring. Phase numbering: group A computes step k in phase 2k and
+// reads its fragments in phase 2k-1; group B reads step k in phase 2k and computes it in 2k+1. Stage
+// k+2 is loaded half by group A (phase 2k-1) and half by group B (phase 2k). Hazards:
+//  - stage k+1 is first read in phase 2k+1; its halves were issued in phases 2k-3 and 2k-2, and each
+//    wave's newer batch (stage k+2) is the only one it leaves in flight at a barrier (vmcnt <= batch).
+//  - stage k+2 overwrites buffer (k-1) % 3, last read in phase 2k-2 (group B), before phase 2k-1.
+template <int WM, int WN, int RM, int RN>
+struct PingPongShape {
+    static constexpr int kWaves = WM * WN;
+    static constexpr int kThreads = kWave * kWaves;
+    static constexpr int kBM = 16 * WM * RM;
+    static constexpr int kBN = 16 * WN * RN;
+    static constexpr int kUnitsPerRow = 8;                 // 64 halves of one A row per stage
+    static constexpr int kABytes = kBM * 128;              // A: [row][8 units], units XOR-swizzled per row
+    static constexpr int kBBytes = kBN * 64;               // B: [chunk 4][col][16 bytes]
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kStages = 3;
+    static constexpr int kLdsBytes = kStages * kStageBytes;
+    static constexpr int kAInstr = kABytes / 1024;         // 1 KiB direct loads per stage
+    static constexpr int kBInstr = kBBytes / 1024;
+    static constexpr int kInstr = kAInstr + kBInstr;
+    static constexpr int kPerWave = kInstr / kWaves;       // each wave's share of one stage
+    static_assert(kWaves == 8 && WM % 2 == 0, "two groups of 4 waves, split by rows");
+    static_assert(kInstr % kWaves == 0, "a stage splits evenly over the waves");
+    static_assert(kBN % kWave == 0, "B rows of a chunk are whole wave loads");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+};
+
+template <int WM, int WN, int RM, int RN, bool kE5M2, bool kOutBf16>
+__global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
+void pingpong_kernel(const Params p) {
+    using S = PingPongShape<WM, WN, RM, RN>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int group = wave / 4;        // 0: A (computes first), 1: B
+    const int wave_m = wave / WN;
+    const int wave_n = wave % WN;
+
+    const int tiles_m = (p.M + S::kBM - 1) / S::kBM;
+    const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * S::kBM;
+    const int n0 = tn * S::kBN;
+
+    const rsrc_t a_rsrc = make_rsrc(p.a, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.K) * 2u);
+    const rsrc_t b_rsrc = make_rsrc(p.b, static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u);
+    const int k_chunks = p.K / 16;
+    const int steps = (k_chunks + 3) / 4;
+    const int full_steps = k_chunks / 4;
+
+    // This wave's direct loads of a stage: instructions j = wave + 8 i of the stage's kInstr 1 KiB loads
+    // (A loads first, then B loads, so load i is an A load exactly when i < kAInstr / 8), 16 bytes a lane.
+    constexpr int kAPerWave = S::kAInstr / S::kWaves;
+    static_assert(S::kAInstr % S::kWaves == 0, "A loads split evenly over the waves");
+    const uint32_t b_step = 4u * static_cast<uint32_t>(p.N) * 16u;
+
+    // The memory phase recomputes its per-lane offsets every time: they would otherwise stay live across
+    // the compute phase, which needs every register for accumulators and fragments. The empty asm makes
+    // the lane index opaque, so the compiler cannot hoist the arithmetic out of the loop.
+    auto opaque_lane = [&]() {
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        return l;
+    };
+
+    // This wave's share of stage `st`: loads j = wave + 8 i of the stage's kInstr 1 KiB direct loads
+    // (A loads first, then B loads, so load i is an A load exactly when i < kAInstr / 8), 16 bytes a lane.
+    // Returns the number of loads issued (0 past the last stage).
+    auto refill = [&](int st) -> int {
+        if (st >= steps) return 0;
+        const int l = opaque_lane();
+        uint8_t* base = lds + (st % S::kStages) * S::kStageBytes + wave * 1024;
+        const uint32_t a_soff = static_cast<uint32_t>(st) * 128u;
+        const uint32_t b_soff = static_cast<uint32_t>(st) * b_step;
+        const bool ragged = st >= full_steps;
+#pragma unroll
+        for (int i = 0; i < S::kPerWave; ++i) {
+            const int j = wave + S::kWaves * i;
+            if (i < kAPerWave) {
+                const int unit = j * kWave + l;
+                const int row = unit / S::kUnitsPerRow;
+                const int u = a_unit_phys<S::kUnitsPerRow>(row, unit % S::kUnitsPerRow);
+                const bool ok = m0 + row < p.M && (!ragged || st * 4 + (u >> 1) < k_chunks);
+                const uint32_t off = (static_cast<uint32_t>(m0 + row) * static_cast<uint32_t>(p.K) +
+                                      static_cast<uint32_t>(u * 8)) * 2u;
+                dma16(a_rsrc, base + i * S::kWaves * 1024, ok ? off : kOob, a_soff);
+            } else {
+                const int unit = (j - S::kAInstr) * kWave + l;
+                const int chunk = unit / S::kBN;
+                const int gcol = n0 + unit % S::kBN;
+                const bool ok = gcol < p.N && (!ragged || st * 4 + chunk < k_chunks);
+                const uint32_t off = (static_cast<uint32_t>(chunk) * static_cast<uint32_t>(p.N) +
+                                      static_cast<uint32_t>(gcol)) * 16u;
+                dma16(b_rsrc, base + i * S::kWaves * 1024, ok ? off : kOob, b_soff);
+            }
+        }
+        return S::kPerWave;
+    };
+
+    // Fragments of one 64-deep step: A rows of this wave (two 16-byte halves per 16-row tile) and its
+    // weight columns. When the accumulators leave room (kDecodeEarly) the weight is decoded to fp16 in the
+    // memory phase, so the compute phase is MFMAs only; otherwise the raw bytes are kept and each 16-column
+    // tile is decoded in the compute phase right before its MFMAs.
+    constexpr bool kDecodeEarly = RM * RN <= 16;
+    half8 xa[RM][2];
+    half8 wb[kDecodeEarly ? RN : 1][2];
+    u32x4 braw[kDecodeEarly ? 1 : RN];
+    auto read_fragments = [&](int st) {
+        const int l = opaque_lane();
+        const int g = l >> 4;
+        const int a_row_base = wave_m * 16 * RM + (l & 15);
+        const int b_col_base = wave_n * 16 * RN + (l & 15);
+        const int key = a_swizzle_key<S::kUnitsPerRow>(a_row_base);
+        const uint8_t* base = lds + (st % S::kStages) * S::kStageBytes;
+        const uint8_t* a0 = base + a_row_base * 128 + (((2 * g) ^ key) << 4);
+        const uint8_t* a1 = base + a_row_base * 128 + (((2 * g + 1) ^ key) << 4);
+        const uint8_t* b0 = base + S::kABytes + g * S::kBN * 16 + b_col_base * 16;
+        if constexpr (kDecodeEarly) {
+            u32x4 raw[RN];
+#pragma unroll
+            for (int j = 0; j < RN; ++j) raw[j] = *reinterpret_cast<const u32x4*>(b0 + j * 256);
+#pragma unroll
+            for (int i = 0; i < RM; ++i) {
+                xa[i][0] = *reinterpret_cast<const half8*>(a0 + i * 2048);
+                xa[i][1] = *reinterpret_cast<const half8*>(a1 + i * 2048);
+            }
+#pragma unroll
+            for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(raw[j], wb[j][0], wb[j][1]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < RN; ++j) braw[j] = *reinterpret_cast<const u32x4*>(b0 + j * 256);
+#pragma unroll
+            for (int i = 0; i < RM; ++i) {
+                xa[i][0] = *reinterpret_cast<const half8*>(a0 + i * 2048);
+                xa[i][1] = *reinterpret_cast<const half8*>(a1 + i * 2048);
+            }
+        }
+    };
+
+    f32x4 acc[RM][RN];
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&]() {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int j = 0; j < RN; ++j) {
+                half8 w;
+                if constexpr (kDecodeEarly) {
+                    w = wb[j][s2];
+                } else {
+                    half8 w0, w1;
+                    decode_chunk<kE5M2>(braw[j], w0, w1);
+                    w = s2 == 0 ? w0 : w1;
+                }
+#pragma unroll
+                for (int i = 0; i < RM; ++i) acc[i][j] = mfma16(w, xa[i][s2], acc[i][j]);
+            }
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Barrier after this wave's loads older than its newest batch (`newest` loads) have landed.
+    auto sync = [&](int newest) {
+        if (newest == S::kPerWave) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kPerWave));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        barrier_only();
+    };
+
+    // Prologue: both groups load their shares of stages 0 and 1, then run the phases. Phase ph is a
+    // compute phase of group A when ph is even and of group B when ph is odd; the other group's memory
+    // phase reads the fragments of step (ph + 1 - group) / 2 and loads its half of that step + 2.
+    refill(0);
+    int newest = refill(1);
+    sync(newest);
+    for (int ph = -1; ph < 2 * steps; ++ph) {
+        if (((ph + group) & 1) == 0) {
+            if (ph >= group) compute();  // group B has no fragments before phase 0 (its first compute is step 0 at phase 1)
+        } else {
+            const int step = (ph + 1 - group) >> 1;
+            if (step < steps) {
+                newest = refill(step + 2);
+                read_fragments(step);
+            } else {
+                newest = 0;
+            }
+        }
+        sync(newest);
+    }
+
+    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
+}
+
 // ---- stream kernel: split-K, global -> VGPR ----------------------------------------------------------------
 
 template <int KS, int WN, int U, int RM, int RN>

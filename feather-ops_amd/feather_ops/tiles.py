@@ -28,6 +28,9 @@ SCALED_MM_TILES = [
     (2, 4, 4, 4, 4, 1),  # 128 x 256
     (4, 2, 4, 4, 4, 1),  # 256 x 128
     (2, 2, 4, 4, 4, 1),  # 128 x 128
+    (2, 2, 4, 4, 8, 1),  # 128 x 256, 4 waves of 64 x 128, two blocks per CU
+    (2, 2, 4, 8, 4, 1),  # 256 x 128, 4 waves of 128 x 64, two blocks per CU
+    (2, 2, 4, 8, 8, 1),  # 256 x 256, 4 waves of 128 x 128
     (2, 2, 8, 4, 4, 1),  # 128 x 128, 128-deep stages
     (1, 4, 4, 4, 2, 1),  # 64 x 128
     (2, 2, 4, 2, 2, 1),  # 64 x 64
