@@ -35,7 +35,7 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # same counters (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile
 # without a measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
-    (2, 4, 4, 8, 4, 1): (147586 * 2.0 + 184295 * 1.0) * 1024,
+    (2, 2, 4, 4, 8, 1): (213886 * 2.0 + 109890 * 1.0) * 1024,
 }
 
 

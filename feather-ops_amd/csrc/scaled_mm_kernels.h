@@ -10,9 +10,11 @@
 // output types, and the bias is added after the downcast in the output precision (naive.py:34-40).
 //
 // Two kernel families share the fragment layout, the decode and the epilogue:
-//  - ring_kernel   (tile field prefetch = 1): a block owns a BM x BN output tile, waves split it WM x WN,
-//                  and K streams through a double-buffered LDS ring, one 16*U-deep stage at a time. The
-//                  next stage's global loads are in flight while the current stage feeds the MFMAs.
+//  - ring_dma_kernel (tile field prefetch = 1): a block owns a BM x BN output tile, waves split it WM x WN,
+//                  and K streams through an LDS ring of 16*U-deep stages (2 or 3 buffers). Activation and
+//                  weight tiles go from HBM straight into LDS with buffer loads that write LDS (no VGPR
+//                  staging); the next stages are in flight while the current one feeds the MFMAs. bf16
+//                  activations travel as they are and are widened to fp16 per fragment after the LDS read.
 //  - stream_kernel (prefetch = 0): for skinny M. No LDS staging: each wave streams its fragments
 //                  straight from global memory into VGPRs (register double buffer), the block's WM
 //                  waves split K, and a short LDS reduction joins their fp32 partial sums.
@@ -213,33 +215,7 @@ __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[
     }
 }
 
-// ---- ring kernel: LDS double buffer ---------------------------------------------------------------------
-
-template <int WM, int WN, int U, int RM, int RN>
-struct RingShape {
-    static constexpr int kThreads = kWave * WM * WN;
-    static constexpr int kBM = 16 * WM * RM;
-    static constexpr int kBN = 16 * WN * RN;
-    static constexpr int kChunks = U;                 // 16-deep k chunks per stage
-    static constexpr int kGroups = U / 4;             // 64-deep MFMA groups per stage
-    static constexpr int kABytes = kBM * U * 32;      // [chunk][row][16 halves]
-    static constexpr int kBBytes = kBN * U * 16;      // [chunk][col][16 bytes]
-    static constexpr int kStageBytes = kABytes + kBBytes;
-    static constexpr int kLdsBytes = 2 * kStageBytes;
-    static constexpr int kAUnits = kBM * U * 2;       // 16-byte pieces of one A stage
-    static constexpr int kBUnits = kBN * U;           // 16-byte pieces of one B stage
-    static constexpr int kALoads = (kAUnits + kThreads - 1) / kThreads;
-    static constexpr int kBLoads = (kBUnits + kThreads - 1) / kThreads;
-    static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
-    static_assert(kThreads <= 1024, "block size");
-    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
-};
-
-// LDS position of the 16-byte half `s` of row `row`'s chunk: the halves of every eighth row are swapped
-// so that the 16 rows one MFMA operand read touches land on distinct banks.
-__device__ __forceinline__ int a_lds_offset(int chunk, int row, int s, int bm) {
-    return chunk * bm * 32 + row * 32 + ((s ^ ((row >> 3) & 1)) << 4);
-}
+// ---- block -> tile mapping -------------------------------------------------------------------------------
 
 // Tile order: consecutive workgroup ids go to different XCDs, so give each XCD a contiguous run of tiles,
 // and walk tiles in groups of kGroupM tile rows so that the blocks resident on one XCD share A and B panels
@@ -259,159 +235,7 @@ __device__ __forceinline__ void tile_of_block(int bid, int nblocks, int tiles_m,
     tn = in / gm;
 }
 
-template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16>
-__global__ __launch_bounds__(kWave * WM * WN) void ring_kernel(const Params p) {
-    using S = RingShape<WM, WN, U, RM, RN>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLdsBytes];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int wave_m = wave / WN;
-    const int wave_n = wave % WN;
-
-    const int tiles_m = (p.M + S::kBM - 1) / S::kBM;
-    const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
-    int tm, tn;
-    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * S::kBM;
-    const int n0 = tn * S::kBN;
-
-    const uint32_t a_bytes = static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.K) * 2u;
-    const uint32_t b_bytes = static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u;
-    const rsrc_t a_rsrc = make_rsrc(p.a, a_bytes);
-    const rsrc_t b_rsrc = make_rsrc(p.b, b_bytes);
-    const int k_chunks = p.K / 16;
-    const int stages = (p.K + 16 * U - 1) / (16 * U);
-
-    // Per-thread global offsets of its share of a stage (stage 0), and where they land in LDS.
-    uint32_t a_goff[S::kALoads];
-    int a_loff[S::kALoads];
-    int a_chunk[S::kALoads];
-    bool a_valid[S::kALoads];
-#pragma unroll
-    for (int i = 0; i < S::kALoads; ++i) {
-        const int u = tid + i * S::kThreads;
-        const int row = u / (2 * U);
-        const int c = u % (2 * U);
-        const int chunk = c >> 1;
-        const int s = c & 1;
-        a_valid[i] = u < S::kAUnits;
-        a_chunk[i] = chunk;
-        const int grow = m0 + row;
-        a_goff[i] = grow < p.M ? (static_cast<uint32_t>(grow) * static_cast<uint32_t>(p.K) +
-                                  static_cast<uint32_t>(chunk * 16 + s * 8)) * 2u
-                               : kOob;
-        a_loff[i] = a_lds_offset(chunk, row, s, S::kBM);
-    }
-    uint32_t b_goff[S::kBLoads];
-    int b_loff[S::kBLoads];
-    int b_chunk[S::kBLoads];
-    bool b_valid[S::kBLoads];
-#pragma unroll
-    for (int i = 0; i < S::kBLoads; ++i) {
-        const int u = tid + i * S::kThreads;
-        const int chunk = u / S::kBN;
-        const int col = u % S::kBN;
-        b_valid[i] = u < S::kBUnits;
-        b_chunk[i] = chunk;
-        const int gcol = n0 + col;
-        b_goff[i] = gcol < p.N ? (static_cast<uint32_t>(chunk) * static_cast<uint32_t>(p.N) +
-                                  static_cast<uint32_t>(gcol)) * 16u
-                               : kOob;
-        b_loff[i] = S::kABytes + chunk * S::kBN * 16 + col * 16;
-    }
-
-    u32x4 a_reg[S::kALoads];
-    u32x4 b_reg[S::kBLoads];
-
-    auto fetch = [&](int stage) {
-        const int chunk0 = stage * U;
-#pragma unroll
-        for (int i = 0; i < S::kALoads; ++i) {
-            const bool in_k = chunk0 + a_chunk[i] < k_chunks;
-            const uint32_t off = (a_goff[i] == kOob || !in_k) ? kOob : a_goff[i] + static_cast<uint32_t>(chunk0) * 32u;
-            a_reg[i] = buf_load16(a_rsrc, off);
-        }
-#pragma unroll
-        for (int i = 0; i < S::kBLoads; ++i) {
-            const bool in_k = chunk0 + b_chunk[i] < k_chunks;
-            const uint32_t off = (b_goff[i] == kOob || !in_k)
-                                     ? kOob
-                                     : b_goff[i] + static_cast<uint32_t>(chunk0) * static_cast<uint32_t>(p.N) * 16u;
-            b_reg[i] = buf_load16(b_rsrc, off);
-        }
-    };
-    auto deposit = [&](int buf) {
-        uint8_t* base = lds + buf * S::kStageBytes;
-#pragma unroll
-        for (int i = 0; i < S::kALoads; ++i) {
-            if (S::kAUnits % S::kThreads == 0 || a_valid[i]) {
-                u32x4 v = a_reg[i];
-                if constexpr (kABf16) v = bf16x8_to_f16x8(v);
-                *reinterpret_cast<u32x4*>(base + a_loff[i]) = v;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < S::kBLoads; ++i) {
-            if (S::kBUnits % S::kThreads == 0 || b_valid[i]) {
-                *reinterpret_cast<u32x4*>(base + b_loff[i]) = b_reg[i];
-            }
-        }
-    };
-
-    f32x4 acc[RM][RN];
-#pragma unroll
-    for (int i = 0; i < RM; ++i)
-#pragma unroll
-        for (int j = 0; j < RN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int g = lane >> 4;       // lane group: which 16-deep chunk of a 64-deep group
-    const int r16 = lane & 15;     // row (A) / column (B) within a 16-wide fragment
-    const int a_row_base = wave_m * 16 * RM + r16;
-    const int b_col_base = wave_n * 16 * RN + r16;
-
-    fetch(0);
-    deposit(0);
-    __syncthreads();
-
-    for (int t = 0; t < stages; ++t) {
-        const bool more = t + 1 < stages;
-        if (more) fetch(t + 1);
-        const uint8_t* base = lds + (t & 1) * S::kStageBytes;
-#pragma unroll
-        for (int q = 0; q < S::kGroups; ++q) {
-            const int chunk = 4 * q + g;
-            half8 xa[RM][2];
-#pragma unroll
-            for (int i = 0; i < RM; ++i) {
-                const int row = a_row_base + 16 * i;
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    xa[i][s] = *reinterpret_cast<const half8*>(base + a_lds_offset(chunk, row, s, S::kBM));
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < RN; ++j) {
-                const int col = b_col_base + 16 * j;
-                const u32x4 raw = *reinterpret_cast<const u32x4*>(base + S::kABytes + chunk * S::kBN * 16 + col * 16);
-                half8 w0, w1;
-                decode_chunk<kE5M2>(raw, w0, w1);
-#pragma unroll
-                for (int i = 0; i < RM; ++i) {
-                    acc[i][j] = mfma16(w0, xa[i][0], acc[i][j]);
-                    acc[i][j] = mfma16(w1, xa[i][1], acc[i][j]);
-                }
-            }
-        }
-        if (more) deposit((t + 1) & 1);
-        __syncthreads();
-    }
-
-    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
-}
-
-// ---- ring kernel with direct-to-LDS loads (fp16 activations) -------------------------------------------------
+// ---- ring kernel: direct-to-LDS loads, LDS ring of 64-deep stages -----------------------------------------
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of this wave are outstanding
 // and leaves the other counters alone (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
@@ -481,7 +305,7 @@ __device__ __forceinline__ int a_unit_phys(int row, int u) {
     return u ^ a_swizzle_key<kUnits>(row);
 }
 
-template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kOutBf16>
+template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16>
 __global__ __launch_bounds__(kWave * WM * WN)
 __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) void ring_dma_kernel(const Params p) {
     using S = DmaShape<WM, WN, U, RM, RN>;
@@ -605,8 +429,10 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
                 }
 #pragma unroll
                 for (int i = 0; i < RM; ++i) {
-                    const half8 x = *reinterpret_cast<const half8*>(
+                    // bf16 rows travel to LDS as they are and are widened to fp16 (RNE) per fragment here.
+                    const u32x4 raw = *reinterpret_cast<const u32x4*>(
                         stage_base + a_lane[q][s] + i * 16 * S::kUnitsPerRow * 16);
+                    const half8 x = __builtin_bit_cast(half8, kABf16 ? bf16x8_to_f16x8(raw) : raw);
 #pragma unroll
                     for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
                 }
@@ -635,220 +461,6 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
                 compute(lds + b * S::kStageBytes);
             }
         }
-    }
-
-    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
-}
-
-// ---- ping-pong ring kernel (fp16 activations, 8 waves) ----------------------------------------------------
-//
-// A vector-memory instruction in the instruction stream of a wave that is issuing MFMAs costs that wave
-// about as much issue time as an MFMA, while the same instruction from another wave on the SIMD does not
-// slow the MFMAs down. So the 8 waves split into two groups of 4 (waves 0-3 and 4-7, one of each per
-// SIMD) that alternate every phase: one group runs a pure compute phase (decode + 64 MFMAs on fragments
-// already in registers) while the other runs a memory phase (its share of the direct global->LDS refill
-// and the LDS->register reads of its next 64-deep step). A workgroup barrier separates phases; group B
-// runs one phase behind group A, so the MFMA pipe of every SIMD always has a compute wave.
-//
-// Block tile BM x BN (WM x WN waves, WM even): group A owns rows [0, BM/2), group B rows [BM/2, BM).
-// K steps of 64 go through a 3-buffer LDS ring. Phase numbering: group A computes step k in phase 2k and
-// reads its fragments in phase 2k-1; group B reads step k in phase 2k and computes it in 2k+1. Stage
-// k+2 is loaded half by group A (phase 2k-1) and half by group B (phase 2k). Hazards:
-//  - stage k+1 is first read in phase 2k+1; its halves were issued in phases 2k-3 and 2k-2, and each
-//    wave's newer batch (stage k+2) is the only one it leaves in flight at a barrier (vmcnt <= batch).
-//  - stage k+2 overwrites buffer (k-1) % 3, last read in phase 2k-2 (group B), before phase 2k-1.
-template <int WM, int WN, int RM, int RN>
-struct PingPongShape {
-    static constexpr int kWaves = WM * WN;
-    static constexpr int kThreads = kWave * kWaves;
-    static constexpr int kBM = 16 * WM * RM;
-    static constexpr int kBN = 16 * WN * RN;
-    static constexpr int kUnitsPerRow = 8;                 // 64 halves of one A row per stage
-    static constexpr int kABytes = kBM * 128;              // A: [row][8 units], units XOR-swizzled per row
-    static constexpr int kBBytes = kBN * 64;               // B: [chunk 4][col][16 bytes]
-    static constexpr int kStageBytes = kABytes + kBBytes;
-    static constexpr int kStages = 3;
-    static constexpr int kLdsBytes = kStages * kStageBytes;
-    static constexpr int kAInstr = kABytes / 1024;         // 1 KiB direct loads per stage
-    static constexpr int kBInstr = kBBytes / 1024;
-    static constexpr int kInstr = kAInstr + kBInstr;
-    static constexpr int kPerWave = kInstr / kWaves;       // each wave's share of one stage
-    static_assert(kWaves == 8 && WM % 2 == 0, "two groups of 4 waves, split by rows");
-    static_assert(kInstr % kWaves == 0, "a stage splits evenly over the waves");
-    static_assert(kBN % kWave == 0, "B rows of a chunk are whole wave loads");
-    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
-};
-
-template <int WM, int WN, int RM, int RN, bool kE5M2, bool kOutBf16>
-__global__ __launch_bounds__(kWave * WM * WN) __attribute__((amdgpu_waves_per_eu(2)))
-void pingpong_kernel(const Params p) {
-    using S = PingPongShape<WM, WN, RM, RN>;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int group = wave / 4;        // 0: A (computes first), 1: B
-    const int wave_m = wave / WN;
-    const int wave_n = wave % WN;
-
-    const int tiles_m = (p.M + S::kBM - 1) / S::kBM;
-    const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
-    int tm, tn;
-    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * S::kBM;
-    const int n0 = tn * S::kBN;
-
-    const rsrc_t a_rsrc = make_rsrc(p.a, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.K) * 2u);
-    const rsrc_t b_rsrc = make_rsrc(p.b, static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u);
-    const int k_chunks = p.K / 16;
-    const int steps = (k_chunks + 3) / 4;
-    const int full_steps = k_chunks / 4;
-
-    // This wave's direct loads of a stage: instructions j = wave + 8 i of the stage's kInstr 1 KiB loads
-    // (A loads first, then B loads, so load i is an A load exactly when i < kAInstr / 8), 16 bytes a lane.
-    constexpr int kAPerWave = S::kAInstr / S::kWaves;
-    static_assert(S::kAInstr % S::kWaves == 0, "A loads split evenly over the waves");
-    const uint32_t b_step = 4u * static_cast<uint32_t>(p.N) * 16u;
-
-    // The memory phase recomputes its per-lane offsets every time: they would otherwise stay live across
-    // the compute phase, which needs every register for accumulators and fragments. The empty asm makes
-    // the lane index opaque, so the compiler cannot hoist the arithmetic out of the loop.
-    auto opaque_lane = [&]() {
-        int l = lane;
-        asm volatile("" : "+v"(l));
-        return l;
-    };
-
-    // This wave's share of stage `st`: loads j = wave + 8 i of the stage's kInstr 1 KiB direct loads
-    // (A loads first, then B loads, so load i is an A load exactly when i < kAInstr / 8), 16 bytes a lane.
-    // Returns the number of loads issued (0 past the last stage).
-    auto refill = [&](int st) -> int {
-        if (st >= steps) return 0;
-        const int l = opaque_lane();
-        uint8_t* base = lds + (st % S::kStages) * S::kStageBytes + wave * 1024;
-        const uint32_t a_soff = static_cast<uint32_t>(st) * 128u;
-        const uint32_t b_soff = static_cast<uint32_t>(st) * b_step;
-        const bool ragged = st >= full_steps;
-#pragma unroll
-        for (int i = 0; i < S::kPerWave; ++i) {
-            const int j = wave + S::kWaves * i;
-            if (i < kAPerWave) {
-                const int unit = j * kWave + l;
-                const int row = unit / S::kUnitsPerRow;
-                const int u = a_unit_phys<S::kUnitsPerRow>(row, unit % S::kUnitsPerRow);
-                const bool ok = m0 + row < p.M && (!ragged || st * 4 + (u >> 1) < k_chunks);
-                const uint32_t off = (static_cast<uint32_t>(m0 + row) * static_cast<uint32_t>(p.K) +
-                                      static_cast<uint32_t>(u * 8)) * 2u;
-                dma16(a_rsrc, base + i * S::kWaves * 1024, ok ? off : kOob, a_soff);
-            } else {
-                const int unit = (j - S::kAInstr) * kWave + l;
-                const int chunk = unit / S::kBN;
-                const int gcol = n0 + unit % S::kBN;
-                const bool ok = gcol < p.N && (!ragged || st * 4 + chunk < k_chunks);
-                const uint32_t off = (static_cast<uint32_t>(chunk) * static_cast<uint32_t>(p.N) +
-                                      static_cast<uint32_t>(gcol)) * 16u;
-                dma16(b_rsrc, base + i * S::kWaves * 1024, ok ? off : kOob, b_soff);
-            }
-        }
-        return S::kPerWave;
-    };
-
-    // Fragments of one 64-deep step: A rows of this wave (two 16-byte halves per 16-row tile) and its
-    // weight columns. When the accumulators leave room (kDecodeEarly) the weight is decoded to fp16 in the
-    // memory phase, so the compute phase is MFMAs only; otherwise the raw bytes are kept and each 16-column
-    // tile is decoded in the compute phase right before its MFMAs.
-    constexpr bool kDecodeEarly = RM * RN <= 16;
-    half8 xa[RM][2];
-    half8 wb[kDecodeEarly ? RN : 1][2];
-    u32x4 braw[kDecodeEarly ? 1 : RN];
-    auto read_fragments = [&](int st) {
-        const int l = opaque_lane();
-        const int g = l >> 4;
-        const int a_row_base = wave_m * 16 * RM + (l & 15);
-        const int b_col_base = wave_n * 16 * RN + (l & 15);
-        const int key = a_swizzle_key<S::kUnitsPerRow>(a_row_base);
-        const uint8_t* base = lds + (st % S::kStages) * S::kStageBytes;
-        const uint8_t* a0 = base + a_row_base * 128 + (((2 * g) ^ key) << 4);
-        const uint8_t* a1 = base + a_row_base * 128 + (((2 * g + 1) ^ key) << 4);
-        const uint8_t* b0 = base + S::kABytes + g * S::kBN * 16 + b_col_base * 16;
-        if constexpr (kDecodeEarly) {
-            u32x4 raw[RN];
-#pragma unroll
-            for (int j = 0; j < RN; ++j) raw[j] = *reinterpret_cast<const u32x4*>(b0 + j * 256);
-#pragma unroll
-            for (int i = 0; i < RM; ++i) {
-                xa[i][0] = *reinterpret_cast<const half8*>(a0 + i * 2048);
-                xa[i][1] = *reinterpret_cast<const half8*>(a1 + i * 2048);
-            }
-#pragma unroll
-            for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(raw[j], wb[j][0], wb[j][1]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < RN; ++j) braw[j] = *reinterpret_cast<const u32x4*>(b0 + j * 256);
-#pragma unroll
-            for (int i = 0; i < RM; ++i) {
-                xa[i][0] = *reinterpret_cast<const half8*>(a0 + i * 2048);
-                xa[i][1] = *reinterpret_cast<const half8*>(a1 + i * 2048);
-            }
-        }
-    };
-
-    f32x4 acc[RM][RN];
-#pragma unroll
-    for (int i = 0; i < RM; ++i)
-#pragma unroll
-        for (int j = 0; j < RN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&]() {
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int j = 0; j < RN; ++j) {
-                half8 w;
-                if constexpr (kDecodeEarly) {
-                    w = wb[j][s2];
-                } else {
-                    half8 w0, w1;
-                    decode_chunk<kE5M2>(braw[j], w0, w1);
-                    w = s2 == 0 ? w0 : w1;
-                }
-#pragma unroll
-                for (int i = 0; i < RM; ++i) acc[i][j] = mfma16(w, xa[i][s2], acc[i][j]);
-            }
-        __builtin_amdgcn_s_setprio(0);
-    };
-
-    // Barrier after this wave's loads older than its newest batch (`newest` loads) have landed.
-    auto sync = [&](int newest) {
-        if (newest == S::kPerWave) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kPerWave));
-        } else {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        }
-        barrier_only();
-    };
-
-    // Prologue: both groups load their shares of stages 0 and 1, then run the phases. Phase ph is a
-    // compute phase of group A when ph is even and of group B when ph is odd; the other group's memory
-    // phase reads the fragments of step (ph + 1 - group) / 2 and loads its half of that step + 2.
-    refill(0);
-    int newest = refill(1);
-    sync(newest);
-    for (int ph = -1; ph < 2 * steps; ++ph) {
-        if (((ph + group) & 1) == 0) {
-            if (ph >= group) compute();  // group B has no fragments before phase 0 (its first compute is step 0 at phase 1)
-        } else {
-            const int step = (ph + 1 - group) >> 1;
-            if (step < steps) {
-                newest = refill(step + 2);
-                read_fragments(step);
-            } else {
-                newest = 0;
-            }
-        }
-        sync(newest);
     }
 
     store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);

@@ -25,21 +25,11 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         t.prefetch != (PF != 0)) {
         return false;
     }
-    if constexpr (PF != 0 && !kABf16 && WM * WN == 8 && WM % 2 == 0 && U == 4) {
-        using S = PingPongShape<WM, WN, RM, RN>;
-        const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
-        hipLaunchKernelGGL((pingpong_kernel<WM, WN, RM, RN, kE5M2, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
-                           dim3(S::kThreads), 0, stream, p);
-    } else if constexpr (PF != 0 && !kABf16) {
+    if constexpr (PF != 0) {
         using S = DmaShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
-        hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
-                           dim3(S::kThreads), 0, stream, p);
-    } else if constexpr (PF != 0) {
-        using S = RingShape<WM, WN, U, RM, RN>;
-        const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
-        hipLaunchKernelGGL((ring_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
-                           dim3(S::kThreads), 0, stream, p);
+        hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16>),
+                           dim3(static_cast<uint32_t>(tiles)), dim3(S::kThreads), 0, stream, p);
     } else {
         using S = StreamShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);

@@ -22,15 +22,13 @@ from . import _lib
 from .tiles import gemm_block_sizes
 
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
+_TILE_STREAM_16x16 = (4, 1, 4, 1, 1, 0)
 _TILE_STREAM_16x64 = (4, 1, 4, 1, 4, 0)
-_TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
-_TILE_STREAM_64x64 = (2, 2, 4, 4, 2, 0)
-_TILE_64x64 = (2, 2, 4, 2, 2, 1)
+_TILE_STREAM_16x64_DEEP = (8, 1, 8, 1, 4, 0)
 _TILE_128x128 = (2, 2, 4, 4, 4, 1)
-_TILE_128x256 = (2, 4, 4, 4, 4, 1)
-_TILE_256x256 = (2, 4, 4, 8, 4, 1)
+_TILE_128x256 = (2, 2, 4, 4, 8, 1)
 
-# MI355X: 256 compute units. A launch below about one block per CU leaves the machine partly idle.
+# MI355X: 256 compute units; the 4-wave ring tiles run two blocks per CU.
 _CUS = 256
 
 
@@ -49,21 +47,21 @@ def select_scaled_mm_config(
 ) -> tuple[int, int, int, int, int, int]:
     """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
 
-    Skinny M streams the weight through registers with K split across waves (the weight read is the
-    whole cost there); from 65 rows up the LDS ring takes over, and the tallest tile whose grid still
-    covers the 256 CUs wins, since a bigger tile re-reads fewer panels per FLOP.
+    Fitted on MI355X over the BASELINE cells (sweep of every tile): up to 16 rows the weight stream is the
+    whole cost, so a 16-row split-K streaming tile is used, 64 columns wide (8 K slices when the weight is
+    large) unless that leaves too few blocks, then 16. While the 128 x 128 LDS-ring grid would not cover
+    the 256 CUs, the 16 x 64 streaming tile's extra blocks win (e.g. 256 x 1024 x 1024: 4.9 us vs 12 us).
+    Past that the ring takes over: 128 x 256 tiles (two 4-wave blocks per CU) once they give two blocks
+    per CU, 128 x 128 below that.
     """
     del K, a_dtype, b_dtype, out_dtype
     if M <= 16:
+        if N >= 8192:
+            return _TILE_STREAM_16x64_DEEP
+        return _TILE_STREAM_16x64 if N >= 4096 else _TILE_STREAM_16x16
+    if _blocks(M, N, _TILE_128x128) < _CUS:
         return _TILE_STREAM_16x64
-    if M <= 32:
-        return _TILE_STREAM_32x64
-    if M <= 64:
-        return _TILE_STREAM_64x64
-    for tile in (_TILE_256x256, _TILE_128x256, _TILE_128x128):
-        if _blocks(M, N, tile) >= _CUS:
-            return tile
-    return _TILE_128x128 if _blocks(M, N, _TILE_128x128) >= _CUS // 2 else _TILE_64x64
+    return _TILE_128x256 if _blocks(M, N, _TILE_128x256) >= 2 * _CUS else _TILE_128x128
 
 
 def _launch(

@@ -23,23 +23,26 @@ Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, rep
 
 SCALED_MM_TILES = [
     # LDS ring (prefetch = 1)
-    (2, 4, 4, 8, 4, 1),  # 256 x 256, 8 waves of 128 x 64
-    (4, 2, 4, 4, 8, 1),  # 256 x 256, 8 waves of 64 x 128
-    (2, 4, 4, 4, 4, 1),  # 128 x 256
-    (4, 2, 4, 4, 4, 1),  # 256 x 128
-    (2, 2, 4, 4, 4, 1),  # 128 x 128
     (2, 2, 4, 4, 8, 1),  # 128 x 256, 4 waves of 64 x 128, two blocks per CU
+    (1, 4, 4, 8, 4, 1),  # 128 x 256, 4 waves of 128 x 64, two blocks per CU
     (2, 2, 4, 8, 4, 1),  # 256 x 128, 4 waves of 128 x 64, two blocks per CU
-    (2, 2, 4, 8, 8, 1),  # 256 x 256, 4 waves of 128 x 128
-    (2, 2, 8, 4, 4, 1),  # 128 x 128, 128-deep stages
+    (2, 2, 4, 4, 4, 1),  # 128 x 128, 4 waves of 64 x 64
+    (4, 2, 4, 4, 8, 1),  # 256 x 256, 8 waves of 64 x 128, 3-stage ring
+    (2, 4, 4, 4, 4, 1),  # 128 x 256, 8 waves of 64 x 64
+    (4, 2, 4, 4, 4, 1),  # 256 x 128, 8 waves of 64 x 64
     (1, 4, 4, 4, 2, 1),  # 64 x 128
     (2, 2, 4, 2, 2, 1),  # 64 x 64
     # streaming split-K (prefetch = 0)
     (4, 1, 4, 1, 4, 0),  # 16 x 64, 4 K slices
     (4, 1, 8, 1, 4, 0),  # 16 x 64, 4 K slices, 128-deep steps
     (8, 1, 4, 1, 4, 0),  # 16 x 64, 8 K slices
+    (8, 1, 8, 1, 4, 0),  # 16 x 64, 8 K slices, 128-deep steps
     (4, 2, 4, 1, 2, 0),  # 16 x 64, 4 K slices x 2 column waves
-    (4, 1, 4, 1, 2, 0),  # 16 x 32
+    (4, 1, 4, 1, 2, 0),  # 16 x 32, 4 K slices
+    (8, 1, 4, 1, 2, 0),  # 16 x 32, 8 K slices
+    (4, 1, 4, 1, 1, 0),  # 16 x 16, 4 K slices
+    (8, 1, 4, 1, 1, 0),  # 16 x 16, 8 K slices
+    (8, 2, 4, 1, 1, 0),  # 16 x 32, 8 K slices x 2 column waves
     (2, 2, 4, 2, 2, 0),  # 32 x 64
     (2, 2, 4, 4, 2, 0),  # 64 x 64
 ]
