@@ -250,6 +250,21 @@ __device__ __forceinline__ void barrier_only() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+// Wait until at most newer * kLoads of this wave's vector-memory operations are outstanding, for a runtime
+// newer in [0, N] (s_waitcnt takes an immediate, so the value is selected from compile-time cases).
+template <int N, int kLoads>
+__device__ __forceinline__ void wait_vm_newer(int newer) {
+    if constexpr (N > 0) {
+        if (newer >= N) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(N * kLoads));
+            return;
+        }
+        wait_vm_newer<N - 1, kLoads>(newer);
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+}
+
 // 16 bytes per lane from buffer offset voff + soff straight into LDS at lds_dst + 16 * lane (lds_dst is
 // wave-uniform). soff is a scalar (SGPR) offset, so a per-lane offset computed once can walk K.
 __device__ __forceinline__ void dma16(rsrc_t r, const uint8_t* lds_dst, uint32_t voff, uint32_t soff = 0) {
@@ -264,32 +279,31 @@ struct DmaShape {
     static constexpr int kThreads = kWave * kWaves;
     static constexpr int kBM = 16 * WM * RM;
     static constexpr int kBN = 16 * WN * RN;
-    static constexpr int kGroups = U / 4;
     static constexpr int kUnitsPerRow = 2 * U;            // 16-byte units in one A row of a stage
     static constexpr int kABytes = kBM * U * 32;          // A: [row][2U units], units XOR-swizzled per row
     static constexpr int kBBytes = kBN * U * 16;          // B: [chunk][col][16 bytes]
     static constexpr int kStageBytes = kABytes + kBBytes;
-    // Blocks of up to 4 waves keep a 2-stage ring when that lets two blocks share a CU, so one block's
-    // MFMAs run while the other waits at its barrier; bigger blocks keep 3 stages in flight.
-    static constexpr int kStages = (kWaves <= 4 && 2 * kStageBytes <= 80 * 1024) ? 2 : 3;
+    // Ring slots: blocks of up to 4 waves keep a 2-slot ring so that two or three blocks share a CU (one
+    // block's MFMAs run while another waits at its barrier; measured better than deeper rings with fewer
+    // resident blocks), bigger blocks keep 3 slots.
+    static constexpr int kStages = kWaves <= 4 ? 2 : 3;
     static constexpr int kLdsBytes = kStages * kStageBytes;
     // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two.
-    static constexpr int kWavesPerEu = (kStages == 2 ? 2 : 1) * ((kWaves + 3) / 4);
+    static constexpr int kWavesPerEu = (kWaves <= 4 ? 2 : 1) * ((kWaves + 3) / 4);
     static constexpr int kAInstr = kBM * kUnitsPerRow / kWave / kWaves;   // 1 KiB direct loads per wave
     static constexpr int kBInstr = U * kBN / kWave / kWaves;
     static constexpr int kLoadsPerStage = kAInstr + kBInstr;
     static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
     static_assert(kBM * kUnitsPerRow % (kWave * kWaves) == 0, "A stage splits into whole wave loads");
     static_assert(kBN % kWave == 0 && (U * kBN / kWave) % kWaves == 0, "B stage splits into whole wave loads");
-    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
-    static_assert(kLoadsPerStage < 64, "vmcnt range");
+    static_assert(kLoadsPerStage * (kStages - 1) < 64, "vmcnt range");
 };
 
 // Physical 16-byte unit of logical unit u in A row `row`. The XOR key depends on row mod 16 only, so it is
-// the same for every 16-row fragment a lane reads and folds into one per-lane base address. With 8
-// units per row (128-byte rows) the key (r ^ (r >> 3)) & 7 gives the 16 rows one fragment read touches
-// 16 distinct bank groups whether the LDS serves 8 or 16 lanes of a 16-byte read per cycle; wider rows
-// use r itself.
+// the same for every 16-row fragment a lane reads and folds into one per-lane base address. The keys give
+// the 16 rows one fragment read touches 16 distinct bank groups whether the LDS serves 8 or 16 lanes of a
+// 16-byte read per cycle: with 8 units per row (128-byte rows) (r ^ (r >> 3)) & 7, wider rows r itself.
 template <int kUnits>
 __device__ __forceinline__ int a_swizzle_key(int row) {
     const int r = row & 15;
@@ -399,12 +413,14 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
     const int b_col_base = wave_n * 16 * RN + r16;
 
     // Per-lane LDS byte offsets within a stage; everything else is a compile-time immediate. Lane group g
-    // reads chunk 4q + g of the stage, whose two 16-byte halves (s = 0, 1) sit at units (8q + 2g + s) ^ key
-    // of the row; the key depends on the lane only (row mod 16), so each (q, s) needs one base register.
+    // reads chunk 4q + g of the stage, whose two 16-byte halves (s = 0, 1) feed the group's two MFMAs and
+    // sit at units (8q + 2g + s) ^ key of the row; the key depends on the lane only (row mod 16), so each
+    // (q, s) needs one base register.
     const int key = a_swizzle_key<S::kUnitsPerRow>(a_row_base);
-    int a_lane[S::kGroups][2];
+    constexpr int kGroups = U / 4;
+    int a_lane[kGroups][2];
 #pragma unroll
-    for (int q = 0; q < S::kGroups; ++q)
+    for (int q = 0; q < kGroups; ++q)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
             a_lane[q][s2] = a_row_base * (S::kUnitsPerRow * 16) + (((8 * q + 2 * g + s2) ^ key) << 4);
@@ -412,26 +428,26 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
 
     auto compute = [&](const uint8_t* stage_base) {
 #pragma unroll
-        for (int q = 0; q < S::kGroups; ++q) {
+        for (int q = 0; q < kGroups; ++q) {
             u32x4 braw[RN];
 #pragma unroll
             for (int j = 0; j < RN; ++j) {
                 braw[j] = *reinterpret_cast<const u32x4*>(stage_base + b_lane + (4 * q * S::kBN + 16 * j) * 16);
             }
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
+            for (int s2 = 0; s2 < 2; ++s2) {
                 half8 w[RN];
 #pragma unroll
                 for (int j = 0; j < RN; ++j) {
                     half8 w0, w1;
                     decode_chunk<kE5M2>(braw[j], w0, w1);
-                    w[j] = s == 0 ? w0 : w1;
+                    w[j] = s2 == 0 ? w0 : w1;
                 }
 #pragma unroll
                 for (int i = 0; i < RM; ++i) {
                     // bf16 rows travel to LDS as they are and are widened to fp16 (RNE) per fragment here.
                     const u32x4 raw = *reinterpret_cast<const u32x4*>(
-                        stage_base + a_lane[q][s] + i * 16 * S::kUnitsPerRow * 16);
+                        stage_base + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
                     const half8 x = __builtin_bit_cast(half8, kABf16 ? bf16x8_to_f16x8(raw) : raw);
 #pragma unroll
                     for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
@@ -440,8 +456,16 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
         }
     };
 
-    issue(0);
-    if (S::kStages == 3 && stages > 1) issue(1);
+    // Wait until this wave's loads of stage t have landed: the newer stages up to t + kStages - 2 (those
+    // already issued) may stay in flight.
+    auto wait_stage = [&](int t) {
+        wait_vm_newer<S::kStages - 2, S::kLoadsPerStage>(stages - 1 - t);
+    };
+
+#pragma unroll
+    for (int t = 0; t < S::kStages - 1; ++t) {
+        if (t < stages) issue(t);
+    }
 
     // One trip of the ring per outer iteration, so every stage's buffer is a compile-time offset.
     for (int t0 = 0; t0 < stages; t0 += S::kStages) {
@@ -451,11 +475,7 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
             if (t < stages) {
                 // Stage t's loads are this wave's oldest; the barrier then makes every wave's share visible
                 // and retires all reads of the buffer the next issued stage reuses (it held stage t - 1).
-                if (S::kStages == 3 && t + 1 < stages) {
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerStage));
-                } else {
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-                }
+                wait_stage(t);
                 barrier_only();
                 if (t + S::kStages - 1 < stages) issue(t + S::kStages - 1);
                 compute(lds + b * S::kStageBytes);

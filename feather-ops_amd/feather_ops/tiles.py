@@ -13,8 +13,9 @@ Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, rep
   `block_m = 16 * warps_m * repeat_m`, `block_n = 16 * warps_n * repeat_n` and `chunk_k = 16 * unroll_k`
   keep their meaning; `unroll_k` must be a multiple of 4 (whole 64-deep MFMA groups).
 - `prefetch = 1` selects the LDS ring kernel: `warps_m x warps_n` waves each own a
-  `16*repeat_m x 16*repeat_n` sub-tile, and K streams through a double-buffered LDS ring of `chunk_k`-deep
-  stages whose next stage is in flight while the current one feeds the MFMAs.
+  `16*repeat_m x 16*repeat_n` sub-tile, and K streams through an LDS ring of `chunk_k`-deep stages (2 slots
+  for blocks of up to 4 waves, so two or three blocks share a CU; 3 slots for 8-wave blocks) whose next
+  stages are in flight while the current one feeds the MFMAs.
 - `prefetch = 0` selects the streaming kernel for skinny M: no LDS staging. The block's `warps_m` waves
   split K instead of M (so `block_m = 16 * repeat_m`), its `warps_n` waves split N, and each wave streams
   its operands from HBM into registers `chunk_k` at a time, double-buffered; a short LDS reduction joins
@@ -54,6 +55,11 @@ def gemm_block_sizes(tile: tuple[int, ...]) -> tuple[int, int, int]:
     prefetch = tile[5] if len(tile) > 5 else 1
     block_m = 16 * repeat_m if prefetch == 0 else 16 * warps_m * repeat_m
     return block_m, 16 * warps_n * repeat_n, 16 * unroll_k
+
+
+def ring_stages(tile: tuple[int, ...]) -> int:
+    """LDS ring slots of a `prefetch = 1` tile: 2 for blocks of up to 4 waves, 3 for bigger blocks."""
+    return 2 if tile[0] * tile[1] <= 4 else 3
 
 
 def threads_per_block(tile: tuple[int, ...]) -> int:

@@ -31,17 +31,18 @@ def test_no_duplicate_tiles():
 
 
 def test_tiles_fit_gfx950():
-    from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, threads_per_block
+    from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, ring_stages, threads_per_block
 
     for tile in SCALED_MM_TILES:
         wm, wn, u, rm, rn, pf = tile
         assert pf in (0, 1)
-        assert u % 4 == 0, tile  # whole 64-deep MFMA groups
         assert threads_per_block(tile) <= 1024, tile
         bm, bn, ck = gemm_block_sizes(tile)
         if pf:
-            lds = 2 * (bm * ck * 2 + bn * ck)  # double-buffered A (fp16) + B (fp8) stages
+            assert u % 4 == 0, tile  # whole 64-deep MFMA groups
+            lds = ring_stages(tile) * (bm * ck * 2 + bn * ck)  # ring of A (2-byte) + B (fp8) stages
         else:
+            assert u % 4 == 0, tile  # the streaming kernel works in 64-deep groups
             lds = (wm - 1) * wn * rm * rn * 64 * 16  # K-slice reduction buffer
         assert lds <= 160 * 1024, tile
 
