@@ -187,13 +187,34 @@ __device__ __forceinline__ f32x4 mfma16(half8 w, half8 x, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(w, x, acc, 0, 0, 0);
 }
 
+// The per-tensor weight scale, read once at kernel start so that its latency hides under the main loop.
+__device__ __forceinline__ float load_scale(const Params& p) {
+    return p.scale ? *p.scale : 1.0f;
+}
+
+// Bias bits of the 4 columns each lane stores in each of a wave's RN column tiles, all loads issued
+// together (one round trip for the wave). Zero when there is no bias.
+template <int RN>
+__device__ __forceinline__ void load_bias(const Params& p, int col0, int lane, u32x2 (&bias_bits)[RN]) {
+    const int c_in = 4 * (lane >> 4);
+    if (p.bias) {
+        const rsrc_t bias_rsrc = make_rsrc(p.bias, static_cast<uint32_t>(p.N) * 2u);
+#pragma unroll
+        for (int j = 0; j < RN; ++j) {
+            const int col = col0 + 16 * j + c_in;
+            bias_bits[j] = buf_load8(bias_rsrc, col < p.N ? static_cast<uint32_t>(col) * 2u : kOob);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RN; ++j) bias_bits[j] = u32x2{0u, 0u};
+    }
+}
+
 // Store one wave's RM x RN accumulator tiles. rows0/cols0: the wave's first output row and column.
 template <int RM, int RN, bool kOutBf16>
 __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[RM][RN], int row0, int col0,
-                                            int lane) {
+                                            int lane, float scale, const u32x2 (&bias_bits)[RN]) {
     const rsrc_t c_rsrc = make_rsrc(p.c, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.N) * 2u);
-    const rsrc_t bias_rsrc = make_rsrc(p.bias, p.bias ? static_cast<uint32_t>(p.N) * 2u : 0u);
-    const float scale = p.scale ? *p.scale : 1.0f;
     const bool has_bias = p.bias != nullptr;
     const int r_in = lane & 15;
     const int c_in = 4 * (lane >> 4);
@@ -201,8 +222,6 @@ __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[
     for (int j = 0; j < RN; ++j) {
         const int col = col0 + 16 * j + c_in;
         const bool col_ok = col < p.N;
-        u32x2 bias_bits{0u, 0u};
-        if (has_bias) bias_bits = buf_load8(bias_rsrc, col_ok ? static_cast<uint32_t>(col) * 2u : kOob);
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
             const int row = row0 + 16 * i + r_in;
@@ -210,7 +229,7 @@ __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[
             const uint32_t off = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.N) +
                                        static_cast<uint32_t>(col)) * 2u
                                     : kOob;
-            buf_store8(epilogue4<kOutBf16>(acc[i][j], scale, has_bias, bias_bits), c_rsrc, off);
+            buf_store8(epilogue4<kOutBf16>(acc[i][j], scale, has_bias, bias_bits[j]), c_rsrc, off);
         }
     }
 }
@@ -250,16 +269,30 @@ __device__ __forceinline__ void barrier_only() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-// Wait until at most newer * kLoads of this wave's vector-memory operations are outstanding, for a runtime
-// newer in [0, N] (s_waitcnt takes an immediate, so the value is selected from compile-time cases).
-template <int N, int kLoads>
-__device__ __forceinline__ void wait_vm_newer(int newer) {
-    if constexpr (N > 0) {
-        if (newer >= N) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(N * kLoads));
+// Ring schedule shared by the host-side tile checks and the kernel: A stage t lands in A slot t % SA and is
+// issued LA = SA - 1 stages ahead, B stage t in B slot t % SB, LB = SB - 1 ahead (LB >= LA). Iteration u
+// issues A(u + LA) and then B(u + LB); the prologue runs the same pattern for u = -LB .. -1. Returns how
+// many of this wave's loads were issued after both A(t) and B(t), up to the end of iteration t - 1, when r
+// stages follow t: the vmcnt that waits for stage t and nothing newer (loads retire in issue order).
+constexpr int ring_loads_after(int LA, int LB, int nA, int nB, int r) {
+    int count = 0;
+    if (LB > LA && LB - LA <= r) count += nB;  // B(t - LA + LB), issued right after A(t)
+    for (int d = 1; d < LA; ++d) {             // iteration t - LA + d: A(t + d), B(t + d + LB - LA)
+        if (d <= r) count += nA;
+        if (d + LB - LA <= r) count += nB;
+    }
+    return count;
+}
+
+// s_waitcnt for stage t given r = stages - 1 - t (an immediate per case; r >= R covers every larger r).
+template <int LA, int LB, int nA, int nB, int R = LB>
+__device__ __forceinline__ void wait_ring_stage(int r) {
+    if constexpr (R > 0) {
+        if (r >= R) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(ring_loads_after(LA, LB, nA, nB, R)));
             return;
         }
-        wait_vm_newer<N - 1, kLoads>(newer);
+        wait_ring_stage<LA, LB, nA, nB, R - 1>(r);
     } else {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
@@ -283,21 +316,30 @@ struct DmaShape {
     static constexpr int kABytes = kBM * U * 32;          // A: [row][2U units], units XOR-swizzled per row
     static constexpr int kBBytes = kBN * U * 16;          // B: [chunk][col][16 bytes]
     static constexpr int kStageBytes = kABytes + kBBytes;
-    // Ring slots: blocks of up to 4 waves keep a 2-slot ring so that two or three blocks share a CU (one
-    // block's MFMAs run while another waits at its barrier; measured better than deeper rings with fewer
-    // resident blocks), bigger blocks keep 3 slots.
-    static constexpr int kStages = kWaves <= 4 ? 2 : 3;
-    static constexpr int kLdsBytes = kStages * kStageBytes;
+    // Ring slots. Blocks of up to 4 waves keep 2 A slots within 80 KiB so that two or three blocks share a CU
+    // (one block's MFMAs run while another waits at its barrier); bigger blocks keep 3 A slots in 160 KiB.
+    // The weight ring gets one slot more (one more stage in flight) when that fits the budget and the tile
+    // is already limited to that many blocks per CU: weight tiles are shared by fewer co-resident blocks
+    // than activation tiles, so their loads miss L2 more often and need the longer lead.
+    static constexpr int kSlotsA = kWaves <= 4 ? 2 : 3;
+    static constexpr int kBudget = (kWaves <= 4 ? 80 : 160) * 1024;
+    static constexpr bool kDeepB = kSlotsA * kABytes + (kSlotsA + 1) * kBBytes <= kBudget &&
+                                   (kWaves > 4 || 2 * kStageBytes > 160 * 1024 / 3);
+    static constexpr int kSlotsB = kSlotsA + (kDeepB ? 1 : 0);
+    static constexpr int kLeadA = kSlotsA - 1;
+    static constexpr int kLeadB = kSlotsB - 1;
+    static constexpr int kPeriod = kSlotsA * kSlotsB / (kSlotsA == kSlotsB ? kSlotsA : 1);  // lcm (coprime or equal)
+    static constexpr int kBRing = kSlotsA * kABytes;  // LDS offset of the B ring
+    static constexpr int kLdsBytes = kSlotsA * kABytes + kSlotsB * kBBytes;
     // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two.
     static constexpr int kWavesPerEu = (kWaves <= 4 ? 2 : 1) * ((kWaves + 3) / 4);
     static constexpr int kAInstr = kBM * kUnitsPerRow / kWave / kWaves;   // 1 KiB direct loads per wave
     static constexpr int kBInstr = U * kBN / kWave / kWaves;
-    static constexpr int kLoadsPerStage = kAInstr + kBInstr;
     static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
     static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
     static_assert(kBM * kUnitsPerRow % (kWave * kWaves) == 0, "A stage splits into whole wave loads");
     static_assert(kBN % kWave == 0 && (U * kBN / kWave) % kWaves == 0, "B stage splits into whole wave loads");
-    static_assert(kLoadsPerStage * (kStages - 1) < 64, "vmcnt range");
+    static_assert(ring_loads_after(kLeadA, kLeadB, kAInstr, kBInstr, kLeadB) < 64, "vmcnt range");
 };
 
 // Physical 16-byte unit of logical unit u in A row `row`. The XOR key depends on row mod 16 only, so it is
@@ -342,6 +384,7 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
     const rsrc_t b_rsrc = make_rsrc(p.b, static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u);
     const int k_chunks = p.K / 16;
     const int stages = (p.K + 16 * U - 1) / (16 * U);
+    const float scale = load_scale(p);
     const int full_stages = k_chunks / U;  // stages with every chunk inside K
 
     // Direct loads: instruction i of this wave fills 1 KiB of LDS, lane l the l-th 16 bytes of it. The
@@ -374,29 +417,32 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
     }
     const uint32_t b_stage_stride = static_cast<uint32_t>(U) * static_cast<uint32_t>(p.N) * 16u;
 
-    auto issue = [&](int stage) {
-        uint8_t* base = lds + (stage % S::kStages) * S::kStageBytes;
-        const uint32_t a_soff = static_cast<uint32_t>(stage) * static_cast<uint32_t>(U) * 32u;
-        const uint32_t b_soff = static_cast<uint32_t>(stage) * b_stage_stride;
+    // Stages at or past full_stages are the ragged last one: chunks past K read zeros.
+    auto issue_a = [&](int stage) {
+        uint8_t* base = lds + (stage % S::kSlotsA) * S::kABytes;
+        const uint32_t soff = static_cast<uint32_t>(stage) * static_cast<uint32_t>(U) * 32u;
         if (stage < full_stages) {
 #pragma unroll
-            for (int i = 0; i < S::kAInstr; ++i) dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, a_off[i], a_soff);
-#pragma unroll
-            for (int i = 0; i < S::kBInstr; ++i) {
-                dma16(b_rsrc, base + S::kABytes + (wave + i * S::kWaves) * 1024, b_off[i], b_soff);
-            }
+            for (int i = 0; i < S::kAInstr; ++i) dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, a_off[i], soff);
         } else {
-            // The ragged last stage: chunks past K read zeros.
-            const int chunk0 = stage * U;
 #pragma unroll
             for (int i = 0; i < S::kAInstr; ++i) {
-                const bool ok = chunk0 + a_chunk[i] < k_chunks;
-                dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? a_off[i] : kOob, a_soff);
+                const bool ok = stage * U + a_chunk[i] < k_chunks;
+                dma16(a_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? a_off[i] : kOob, soff);
             }
+        }
+    };
+    auto issue_b = [&](int stage) {
+        uint8_t* base = lds + S::kBRing + (stage % S::kSlotsB) * S::kBBytes;
+        const uint32_t soff = static_cast<uint32_t>(stage) * b_stage_stride;
+        if (stage < full_stages) {
+#pragma unroll
+            for (int i = 0; i < S::kBInstr; ++i) dma16(b_rsrc, base + (wave + i * S::kWaves) * 1024, b_off[i], soff);
+        } else {
 #pragma unroll
             for (int i = 0; i < S::kBInstr; ++i) {
-                const bool ok = chunk0 + b_chunk[i] < k_chunks;
-                dma16(b_rsrc, base + S::kABytes + (wave + i * S::kWaves) * 1024, ok ? b_off[i] : kOob, b_soff);
+                const bool ok = stage * U + b_chunk[i] < k_chunks;
+                dma16(b_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? b_off[i] : kOob, soff);
             }
         }
     };
@@ -424,15 +470,15 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
             a_lane[q][s2] = a_row_base * (S::kUnitsPerRow * 16) + (((8 * q + 2 * g + s2) ^ key) << 4);
-    const int b_lane = S::kABytes + g * S::kBN * 16 + b_col_base * 16;
+    const int b_lane = g * S::kBN * 16 + b_col_base * 16;
 
-    auto compute = [&](const uint8_t* stage_base) {
+    auto compute = [&](const uint8_t* a_stage, const uint8_t* b_stage) {
 #pragma unroll
         for (int q = 0; q < kGroups; ++q) {
             u32x4 braw[RN];
 #pragma unroll
             for (int j = 0; j < RN; ++j) {
-                braw[j] = *reinterpret_cast<const u32x4*>(stage_base + b_lane + (4 * q * S::kBN + 16 * j) * 16);
+                braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + (4 * q * S::kBN + 16 * j) * 16);
             }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
@@ -447,7 +493,7 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
                 for (int i = 0; i < RM; ++i) {
                     // bf16 rows travel to LDS as they are and are widened to fp16 (RNE) per fragment here.
                     const u32x4 raw = *reinterpret_cast<const u32x4*>(
-                        stage_base + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
+                        a_stage + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
                     const half8 x = __builtin_bit_cast(half8, kABf16 ? bf16x8_to_f16x8(raw) : raw);
 #pragma unroll
                     for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
@@ -456,34 +502,33 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
         }
     };
 
-    // Wait until this wave's loads of stage t have landed: the newer stages up to t + kStages - 2 (those
-    // already issued) may stay in flight.
-    auto wait_stage = [&](int t) {
-        wait_vm_newer<S::kStages - 2, S::kLoadsPerStage>(stages - 1 - t);
-    };
-
+    // Prologue: iterations -LB .. -1 of the issue pattern.
 #pragma unroll
-    for (int t = 0; t < S::kStages - 1; ++t) {
-        if (t < stages) issue(t);
+    for (int u = -S::kLeadB; u < 0; ++u) {
+        if (u + S::kLeadA >= 0 && u + S::kLeadA < stages) issue_a(u + S::kLeadA);
+        if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
     }
 
-    // One trip of the ring per outer iteration, so every stage's buffer is a compile-time offset.
-    for (int t0 = 0; t0 < stages; t0 += S::kStages) {
+    // One period of both rings per outer iteration, so every slot is a compile-time offset.
+    for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
 #pragma unroll
-        for (int b = 0; b < S::kStages; ++b) {
+        for (int b = 0; b < S::kPeriod; ++b) {
             const int t = t0 + b;
             if (t < stages) {
-                // Stage t's loads are this wave's oldest; the barrier then makes every wave's share visible
-                // and retires all reads of the buffer the next issued stage reuses (it held stage t - 1).
-                wait_stage(t);
+                // Stage t's loads are complete for this wave; the barrier then makes every wave's share
+                // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
+                wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
                 barrier_only();
-                if (t + S::kStages - 1 < stages) issue(t + S::kStages - 1);
-                compute(lds + b * S::kStageBytes);
+                if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
+                if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
             }
         }
     }
 
-    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane);
+    u32x2 bias_bits[RN];
+    load_bias<RN>(p, n0 + wave_n * 16 * RN, lane, bias_bits);
+    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale, bias_bits);
 }
 
 // ---- stream kernel: split-K, global -> VGPR ----------------------------------------------------------------
@@ -494,7 +539,8 @@ struct StreamShape {
     static constexpr int kBM = 16 * RM;
     static constexpr int kBN = 16 * WN * RN;
     static constexpr int kGroups = U / 4;             // 64-deep groups per iteration of one wave
-    static constexpr int kRedBytes = (KS > 1 ? KS - 1 : 0) * WN * RM * RN * kWave * 16;
+    static constexpr int kFrags = WN * RM * RN;       // 16 x 16 output fragments of the block
+    static constexpr int kRedBytes = (KS > 1 ? KS : 0) * kFrags * kWave * 16;
     static_assert(U % 4 == 0, "an iteration is a whole number of 64-deep MFMA groups");
     static_assert(kThreads <= 1024, "block size");
     static_assert(kRedBytes <= 160 * 1024, "LDS budget of one CU");
@@ -507,10 +553,11 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int ks = wave / WN;          // which K slice this wave reduces
     const int wave_n = wave % WN;
 
+    const float scale = load_scale(p);
     const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
     const int tm = blockIdx.x / tiles_n;
     const int tn = blockIdx.x % tiles_n;
@@ -619,29 +666,31 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
     if (it < iters) consume(f0);
 
     if constexpr (KS > 1) {
-        // Deterministic join of the K slices: slices 1..KS-1 park their sums in LDS, slice 0 adds them
-        // in slice order and runs the epilogue.
+        // Deterministic join of the K slices: every wave parks its sums in LDS, then the block's waves share
+        // the output fragments, each adding a fragment's slices in slice order (0, 1, ..., KS - 1) and
+        // storing it; the fragment's bias loads are in flight during its join.
         f32x4* red = reinterpret_cast<f32x4*>(lds);
-        if (ks > 0) {
 #pragma unroll
-            for (int i = 0; i < RM; ++i)
+        for (int i = 0; i < RM; ++i)
 #pragma unroll
-                for (int j = 0; j < RN; ++j)
-                    red[(((ks - 1) * WN + wave_n) * RM * RN + i * RN + j) * kWave + lane] = acc[i][j];
-        }
+            for (int j = 0; j < RN; ++j)
+                red[(ks * S::kFrags + (wave_n * RM + i) * RN + j) * kWave + lane] = acc[i][j];
         __syncthreads();
-        if (ks == 0) {
+        for (int f = wave; f < S::kFrags; f += KS * WN) {
+            const int i = (f / RN) % RM;
+            const int j = f % RN;
+            const int col0 = tn * S::kBN + (f / (RM * RN)) * 16 * RN + 16 * j;
+            u32x2 bias_bits[1];
+            load_bias<1>(p, col0, lane, bias_bits);
+            f32x4 sum[1][1] = {{red[f * kWave + lane]}};
 #pragma unroll
-            for (int k2 = 1; k2 < KS; ++k2)
-#pragma unroll
-                for (int i = 0; i < RM; ++i)
-#pragma unroll
-                    for (int j = 0; j < RN; ++j)
-                        acc[i][j] += red[(((k2 - 1) * WN + wave_n) * RM * RN + i * RN + j) * kWave + lane];
-            store_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane);
+            for (int k2 = 1; k2 < KS; ++k2) sum[0][0] += red[(k2 * S::kFrags + f) * kWave + lane];
+            store_tiles<1, 1, kOutBf16>(p, sum, m0 + 16 * i, col0, lane, scale, bias_bits);
         }
     } else {
-        store_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane);
+        u32x2 bias_bits[RN];
+        load_bias<RN>(p, n0, lane, bias_bits);
+        store_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane, scale, bias_bits);
     }
 }
 

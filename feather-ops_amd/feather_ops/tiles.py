@@ -13,9 +13,10 @@ Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, rep
   `block_m = 16 * warps_m * repeat_m`, `block_n = 16 * warps_n * repeat_n` and `chunk_k = 16 * unroll_k`
   keep their meaning; `unroll_k` must be a multiple of 4 (whole 64-deep MFMA groups).
 - `prefetch = 1` selects the LDS ring kernel: `warps_m x warps_n` waves each own a
-  `16*repeat_m x 16*repeat_n` sub-tile, and K streams through an LDS ring of `chunk_k`-deep stages (2 slots
-  for blocks of up to 4 waves, so two or three blocks share a CU; 3 slots for 8-wave blocks) whose next
-  stages are in flight while the current one feeds the MFMAs.
+  `16*repeat_m x 16*repeat_n` sub-tile, and K streams through LDS rings of `chunk_k`-deep stages: the
+  activation ring has 2 slots for blocks of up to 4 waves (so two or three blocks share a CU) and 3 for
+  8-wave blocks, and the weight ring one more when it fits (see `ring_slots`), so the next stages are in
+  flight while the current one feeds the MFMAs.
 - `prefetch = 0` selects the streaming kernel for skinny M: no LDS staging. The block's `warps_m` waves
   split K instead of M (so `block_m = 16 * repeat_m`), its `warps_n` waves split N, and each wave streams
   its operands from HBM into registers `chunk_k` at a time, double-buffered; a short LDS reduction joins
@@ -57,9 +58,22 @@ def gemm_block_sizes(tile: tuple[int, ...]) -> tuple[int, int, int]:
     return block_m, 16 * warps_n * repeat_n, 16 * unroll_k
 
 
-def ring_stages(tile: tuple[int, ...]) -> int:
-    """LDS ring slots of a `prefetch = 1` tile: 2 for blocks of up to 4 waves, 3 for bigger blocks."""
-    return 2 if tile[0] * tile[1] <= 4 else 3
+def ring_slots(tile: tuple[int, ...]) -> tuple[int, int]:
+    """(activation, weight) LDS ring slots of a `prefetch = 1` tile, the rule the kernel applies.
+
+    Blocks of up to 4 waves keep 2 activation slots within an 80 KiB budget, bigger blocks 3 within
+    160 KiB; the weight ring gets one more slot when that fits the budget and the tile already runs at
+    most two blocks per CU (8-wave blocks: always when it fits).
+    """
+    warps_m, warps_n, unroll_k, repeat_m, repeat_n = tile[:5]
+    waves = warps_m * warps_n
+    a_bytes = 16 * warps_m * repeat_m * unroll_k * 32
+    b_bytes = 16 * warps_n * repeat_n * unroll_k * 16
+    slots_a = 2 if waves <= 4 else 3
+    budget = (80 if waves <= 4 else 160) * 1024
+    deep_b = slots_a * a_bytes + (slots_a + 1) * b_bytes <= budget and (
+        waves > 4 or 2 * (a_bytes + b_bytes) > 160 * 1024 // 3)
+    return slots_a, slots_a + (1 if deep_b else 0)
 
 
 def threads_per_block(tile: tuple[int, ...]) -> int:

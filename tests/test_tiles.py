@@ -31,7 +31,7 @@ def test_no_duplicate_tiles():
 
 
 def test_tiles_fit_gfx950():
-    from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, ring_stages, threads_per_block
+    from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, ring_slots, threads_per_block
 
     for tile in SCALED_MM_TILES:
         wm, wn, u, rm, rn, pf = tile
@@ -40,11 +40,22 @@ def test_tiles_fit_gfx950():
         bm, bn, ck = gemm_block_sizes(tile)
         if pf:
             assert u % 4 == 0, tile  # whole 64-deep MFMA groups
-            lds = ring_stages(tile) * (bm * ck * 2 + bn * ck)  # ring of A (2-byte) + B (fp8) stages
+            slots_a, slots_b = ring_slots(tile)
+            assert 2 <= slots_a <= slots_b <= slots_a + 1, tile
+            lds = slots_a * bm * ck * 2 + slots_b * bn * ck  # rings of A (2-byte) and B (fp8) stages
         else:
             assert u % 4 == 0, tile  # the streaming kernel works in 64-deep groups
-            lds = (wm - 1) * wn * rm * rn * 64 * 16  # K-slice reduction buffer
+            lds = (wm if wm > 1 else 0) * wn * rm * rn * 64 * 16  # K-slice join buffer
         assert lds <= 160 * 1024, tile
+
+
+def test_ring_slots_rule():
+    from feather_ops.tiles import ring_slots
+
+    assert ring_slots((2, 2, 4, 4, 8, 1)) == (2, 3)  # 128 x 256: 32 + 48 KiB, two blocks per CU
+    assert ring_slots((2, 2, 4, 4, 4, 1)) == (2, 2)  # 128 x 128: keeps three blocks per CU
+    assert ring_slots((2, 2, 4, 8, 4, 1)) == (2, 2)  # 256 x 128: 2 x 32 + 3 x 8 KiB exceeds 80 KiB
+    assert ring_slots((4, 2, 4, 4, 8, 1)) == (3, 4)  # 256 x 256, 8 waves: 96 + 64 KiB
 
 
 def test_tile_shape_formula():
