@@ -262,6 +262,9 @@ constexpr int vmcnt_imm(int n) {
     return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8);
 }
 
+// s_waitcnt immediate that waits for every outstanding LDS operation of this wave (vmcnt left alone).
+constexpr int kLgkm0Imm = 0xf | (0x3 << 14) | (0x7 << 4);
+
 // Workgroup barrier that does not wait for outstanding loads (unlike __syncthreads, whose fence waits
 // for every in-flight load, including the ones filling later ring stages). The memory clobber keeps
 // the compiler from moving LDS accesses across it.
@@ -541,15 +544,23 @@ struct StreamShape {
     static constexpr int kGroups = U / 4;             // 64-deep groups per iteration of one wave
     static constexpr int kFrags = WN * RM * RN;       // 16 x 16 output fragments of the block
     static constexpr int kRedBytes = (KS > 1 ? KS : 0) * kFrags * kWave * 16;
+    // Activations: per wave, a double buffer of one iteration's fragments (16 rows x 64 k x 2 bytes each).
+    static constexpr int kAFragBytes = 2048;
+    static constexpr int kABufBytes = kGroups * RM * kAFragBytes;
+    static constexpr int kAWaveBytes = 2 * kABufBytes;
+    static constexpr int kALdsBytes = KS * WN * kAWaveBytes;
+    static constexpr int kLdsBytes = kALdsBytes + kRedBytes;
+    static constexpr int kLoadsPerFetch = kGroups * (2 * RM + RN);  // vector-memory ops of one fetch
     static_assert(U % 4 == 0, "an iteration is a whole number of 64-deep MFMA groups");
     static_assert(kThreads <= 1024, "block size");
-    static_assert(kRedBytes <= 160 * 1024, "LDS budget of one CU");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+    static_assert(kLoadsPerFetch < 64, "vmcnt range");
 };
 
 template <int KS, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16>
 __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p) {
     using S = StreamShape<KS, WN, U, RM, RN>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kRedBytes > 0 ? S::kRedBytes : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -574,13 +585,32 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
     const int k_chunks = p.K / 16;
     const int groups_total = (k_chunks + 3) / 4;   // 64-deep groups covering K
 
-    // Row / column base offsets (chunk 0); kOob when the row or column is past the edge.
-    uint32_t a_base[RM];
+    // Activation fragments reach this wave's LDS buffer by direct loads of whole 128-byte row segments
+    // (one instruction: 8 rows x 8 units of 16 bytes, unit = 8 consecutive k), so every cache line an
+    // instruction touches is used in full. Unit u of fragment row r sits at slot u ^ key(r), the key of the
+    // ring kernel's A tiles, so the operand reads below are free of bank conflicts. Lane l of half h fills
+    // slot l % 8 of row 8h + l / 8; a_dma[i][h] is its row's offset plus the unit's, kOob past M.
+    uint8_t* const a_lds = lds + wave * S::kAWaveBytes;
+    uint32_t a_dma[RM][2];
+    int a_dma_chunk[2];
 #pragma unroll
-    for (int i = 0; i < RM; ++i) {
-        const int row = m0 + 16 * i + r16;
-        a_base[i] = row < p.M ? static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) * 2u : kOob;
+    for (int h = 0; h < 2; ++h) {
+        const int row_in = 8 * h + (lane >> 3);
+        const int unit = (lane & 7) ^ a_swizzle_key<8>(row_in);
+        a_dma_chunk[h] = unit >> 1;
+#pragma unroll
+        for (int i = 0; i < RM; ++i) {
+            const int row = m0 + 16 * i + row_in;
+            a_dma[i][h] = row < p.M ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) +
+                                       static_cast<uint32_t>(unit * 8)) * 2u
+                                    : kOob;
+        }
     }
+    // Operand reads: lane (g, r16) takes units 2g (s = 0) and 2g + 1 (s = 1) of row r16.
+    int a_rd[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) a_rd[s] = r16 * 128 + (((2 * g + s) ^ a_swizzle_key<8>(r16)) << 4);
+
     uint32_t b_base[RN];
 #pragma unroll
     for (int j = 0; j < RN; ++j) {
@@ -590,25 +620,34 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
     const uint32_t b_chunk_stride = static_cast<uint32_t>(p.N) * 16u;
 
     struct Frag {
-        u32x4 a[S::kGroups][RM][2];
         u32x4 b[S::kGroups][RN];
     };
-    auto fetch = [&](Frag& f, int it) {
+    // One iteration's operands: activations into LDS buffer `buf`, weights into registers. The LDS wait
+    // first retires this wave's reads of the buffer being refilled.
+    auto fetch = [&](Frag& f, int buf, int it) {
+        __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
 #pragma unroll
         for (int q = 0; q < S::kGroups; ++q) {
             const int group = (it * S::kGroups + q) * KS + ks;   // K slices interleave group by group
+            const uint32_t a_soff = static_cast<uint32_t>(group) * 128u;
+            uint8_t* const dst = a_lds + buf * S::kABufBytes + q * RM * S::kAFragBytes;
+            if (4 * group + 3 < k_chunks) {
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, a_dma[i][h], a_soff);
+            } else {
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const bool ok = 4 * group + a_dma_chunk[h] < k_chunks;
+                        dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, ok ? a_dma[i][h] : kOob, a_soff);
+                    }
+            }
             const int chunk = 4 * group + g;
             const bool in_k = chunk < k_chunks;
-#pragma unroll
-            for (int i = 0; i < RM; ++i) {
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const uint32_t off = (a_base[i] == kOob || !in_k)
-                                             ? kOob
-                                             : a_base[i] + static_cast<uint32_t>(chunk * 16 + 8 * s) * 2u;
-                    f.a[q][i][s] = buf_load16(a_rsrc, off);
-                }
-            }
 #pragma unroll
             for (int j = 0; j < RN; ++j) {
                 const uint32_t off = (b_base[j] == kOob || !in_k)
@@ -625,7 +664,7 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
 #pragma unroll
         for (int j = 0; j < RN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto consume = [&](const Frag& f) {
+    auto consume = [&](const Frag& f, int buf) {
 #pragma unroll
         for (int q = 0; q < S::kGroups; ++q) {
             half8 xa[RM][2];
@@ -633,7 +672,8 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             for (int i = 0; i < RM; ++i) {
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    u32x4 v = f.a[q][i][s];
+                    u32x4 v = *reinterpret_cast<const u32x4*>(
+                        a_lds + buf * S::kABufBytes + (q * RM + i) * S::kAFragBytes + a_rd[s]);
                     if constexpr (kABf16) v = bf16x8_to_f16x8(v);
                     xa[i][s] = __builtin_bit_cast(half8, v);
                 }
@@ -651,25 +691,36 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
         }
     };
 
-    // Iterations of this wave: groups ks, ks + KS, ... taken kGroups at a time.
+    // Iterations of this wave: groups ks, ks + KS, ... taken kGroups at a time; fetch it + 1 is in flight
+    // while iteration it computes. Before a consume, this wave's loads of that iteration have landed
+    // (vector-memory operations retire in issue order, so only the newer fetch may stay outstanding).
     const int per_iter = S::kGroups * KS;
     const int iters = (groups_total + per_iter - 1) / per_iter;
     Frag f0, f1;
-    if (iters > 0) fetch(f0, 0);
+    if (iters > 0) fetch(f0, 0, 0);
     int it = 0;
     for (; it + 1 < iters; it += 2) {
-        fetch(f1, it + 1);
-        consume(f0);
-        if (it + 2 < iters) fetch(f0, it + 2);
-        consume(f1);
+        fetch(f1, 1, it + 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
+        consume(f0, 0);
+        if (it + 2 < iters) {
+            fetch(f0, 0, it + 2);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        consume(f1, 1);
     }
-    if (it < iters) consume(f0);
+    if (it < iters) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        consume(f0, 0);
+    }
 
     if constexpr (KS > 1) {
         // Deterministic join of the K slices: every wave parks its sums in LDS, then the block's waves share
         // the output fragments, each adding a fragment's slices in slice order (0, 1, ..., KS - 1) and
         // storing it; the fragment's bias loads are in flight during its join.
-        f32x4* red = reinterpret_cast<f32x4*>(lds);
+        f32x4* red = reinterpret_cast<f32x4*>(lds + S::kALdsBytes);
 #pragma unroll
         for (int i = 0; i < RM; ++i)
 #pragma unroll

@@ -24,7 +24,7 @@ from .tiles import gemm_block_sizes
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
 _TILE_STREAM_16x16 = (4, 1, 4, 1, 1, 0)
 _TILE_STREAM_16x64 = (4, 1, 4, 1, 4, 0)
-_TILE_STREAM_16x64_DEEP = (8, 1, 8, 1, 4, 0)
+_TILE_STREAM_16x64_8SLICE = (8, 1, 4, 1, 4, 0)
 _TILE_128x128 = (2, 2, 4, 4, 4, 1)
 _TILE_128x256 = (2, 2, 4, 4, 8, 1)
 
@@ -47,7 +47,7 @@ def select_scaled_mm_config(
 ) -> tuple[int, int, int, int, int, int]:
     """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
 
-    Fitted on MI355X over the BASELINE cells (sweep of every tile): up to 16 rows the weight stream is the
+    Fitted on MI355X over the benchmark cells (sweep of every tile): up to 16 rows the weight stream is the
     whole cost, so a 16-row split-K streaming tile is used, 64 columns wide (8 K slices when the weight is
     large) unless that leaves too few blocks, then 16. While the 128 x 128 LDS-ring grid would not cover
     the 256 CUs, the 16 x 64 streaming tile's extra blocks win (e.g. 256 x 1024 x 1024: 4.9 us vs 12 us).
@@ -57,7 +57,7 @@ def select_scaled_mm_config(
     del K, a_dtype, b_dtype, out_dtype
     if M <= 16:
         if N >= 8192:
-            return _TILE_STREAM_16x64_DEEP
+            return _TILE_STREAM_16x64_8SLICE
         return _TILE_STREAM_16x64 if N >= 4096 else _TILE_STREAM_16x16
     if _blocks(M, N, _TILE_128x128) < _CUS:
         return _TILE_STREAM_16x64

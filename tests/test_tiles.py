@@ -45,7 +45,8 @@ def test_tiles_fit_gfx950():
             lds = slots_a * bm * ck * 2 + slots_b * bn * ck  # rings of A (2-byte) and B (fp8) stages
         else:
             assert u % 4 == 0, tile  # the streaming kernel works in 64-deep groups
-            lds = (wm if wm > 1 else 0) * wn * rm * rn * 64 * 16  # K-slice join buffer
+            join = (wm if wm > 1 else 0) * wn * rm * rn * 64 * 16  # K-slice join buffer
+            lds = wm * wn * 2 * (u // 4) * rm * 2048 + join  # per-wave activation double buffers + join
         assert lds <= 160 * 1024, tile
 
 
