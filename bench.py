@@ -30,12 +30,13 @@ for p in (ROOT, ROOT / "feather-ops_amd"):
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 
-# HBM bytes per launch of the C3 kernel, by tile: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of
-# `bench.py --only c3` (KiB per dispatch), scaled by the factors a 512 MiB device-to-device copy gives the
-# same counters (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile
-# without a measurement reports null.
+# HBM bytes per launch, by (cell, tile): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of `bench.py --only <cell>`
+# (KiB per dispatch), scaled by the factors a 512 MiB device-to-device copy gives the same counters
+# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile without a
+# measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
-    (2, 2, 4, 4, 8, 1): (213886 * 2.0 + 109890 * 1.0) * 1024,
+    ("c3", (2, 2, 4, 4, 8, 1)): (192487 * 2.0 + 101899 * 1.0) * 1024,
+    ("c4", (8, 1, 4, 1, 4, 0)): (29219 * 2.0 + 448 * 1.0) * 1024,
 }
 
 
@@ -46,18 +47,25 @@ def algorithmic_bytes(m: int, k: int, n: int, bias: bool = False) -> int:
 
 
 def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0):
-    import numpy as np
+    """The benchmark workload, generated on the GPU: A ~ N(0, 1) [M, K] in fp16 or bf16, W ~ N(0, 0.02)
+    [N, K] quantized to e5m2 with the per-tensor scale max|W| / 57344, prepacked by the package's own
+    `prepack_b_for_scaled_mm`. Returns (a, [prepacked weight x copies], scale)."""
     import torch
 
-    from oracle import naive as oracle  # the seeded input recipe (no oracle arithmetic on this path)
+    import feather_ops
 
-    a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, a_fmt, seed=seed)
-    a_dtype = torch.bfloat16 if a_fmt == oracle.BF16 else torch.float16
-    a = torch.from_numpy(a_bits.view(np.int16)).view(a_dtype).cuda()
-    b0 = torch.from_numpy(packed).view(torch.float8_e5m2).cuda()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    a_dtype = torch.bfloat16 if a_fmt == "bf16" else torch.float16
+    a = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float32).to(a_dtype)
+    w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    scale = w.abs().max() / 57344.0
+    w8 = (w / scale).to(torch.float8_e5m2)
+    del w
+    b0 = feather_ops.prepack_b_for_scaled_mm(w8.t().contiguous())
+    del w8
     bs = [b0] + [b0.clone() for _ in range(copies - 1)]
-    s = torch.tensor(scale, dtype=torch.float32, device="cuda")
-    return a, bs, s, (a_bits, packed, scale)
+    return a, bs, scale.reshape(()).to(torch.float32)
 
 
 def time_c3(steps: int, warmup: int):
@@ -66,7 +74,7 @@ def time_c3(steps: int, warmup: int):
     import feather_ops
 
     m, k, n = 4096, 3072, 12288
-    a, bs, s, _ = make_device_inputs(m, k, n, "fp16")
+    a, bs, s = make_device_inputs(m, k, n, "fp16")
     b = bs[0]
     tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, b.dtype, torch.float16)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
@@ -95,7 +103,7 @@ def time_c4(reps: int = 50, copies: int = 8):
     import feather_ops
 
     m, k, n = 16, 4096, 14336
-    a, bs, s, _ = make_device_inputs(m, k, n, "fp16", copies=copies)
+    a, bs, s = make_device_inputs(m, k, n, "fp16", copies=copies)
     tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
     outs = [torch.empty((m, n), dtype=torch.float16, device="cuda") for _ in range(copies)]
     op = torch.ops.feather_ops.scaled_mm.default
@@ -144,7 +152,7 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
         torch.cuda.synchronize()
         return
     m, k, n, copies = (4096, 3072, 12288, 1) if which == "c3" else (16, 4096, 14336, 8)
-    a, bs, s, _ = make_device_inputs(m, k, n, "fp16", copies=copies)
+    a, bs, s = make_device_inputs(m, k, n, "fp16", copies=copies)
     if tile is None:
         tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
@@ -155,13 +163,19 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
 
 
 def time_cpu_oracle(budget_s: float = 10.0):
-    """The oracle on host cores over a row sample of C3, scaled to TFLOP/s of the same workload."""
+    """The oracle on host cores over a row sample of the C3 workload (the same device-generated inputs,
+    copied to the host), scaled to TFLOP/s. The oracle is the checker; it is only timed here."""
     import numpy as np
+    import torch
 
     from oracle import naive as oracle
 
     m, k, n = 4096, 3072, 12288
-    a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, oracle.F16, seed=0)
+    a, bs, s = make_device_inputs(m, k, n, "fp16")
+    a_bits = a.view(torch.int16).cpu().numpy().view(np.uint16)
+    packed = bs[0].view(torch.uint8).cpu().numpy()
+    scale = float(s.item())
+    del a, bs, s
     threads = min(16, oracle.cpu_count())
     rows = 32
     t0 = time.perf_counter()
@@ -222,19 +236,20 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to e5m2 with a per-tensor scale)",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to e5m2 with a per-tensor scale, generated on the GPU)",
         "config": {"workload": "C3 DiT MLP up-projection: fp16 [4096,3072] x e5m2 [12288,3072] -> fp16, scale, no bias",
                    "M": c3["m"], "K": c3["k"], "N": c3["n"], "tile": c3["tile"],
                    "pct_fp16_peak": round(100 * c3["tflops"] / PEAK_FP16_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(c3["tflops"] / PEAK_FP16_TFLOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES.get(tuple(c3["tile"]))},
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(("c3", tuple(c3["tile"])))},
     }
     if c4 is not None:
         line["hbm_cell"] = {"workload": "C4 skinny: fp16 [16,4096] x e5m2 [14336,4096] -> fp16",
                             "GBps": round(c4["gbps"], 1), "us_per_launch": round(c4["us"], 3),
                             "frac_hbm_peak": round(c4["gbps"] / PEAK_HBM_GBPS, 4), "tile": c4["tile"],
-                            "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"]}
+                            "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"],
+                            "traffic": MEASURED_TRAFFIC_BYTES.get(("c4", tuple(c4["tile"])))}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))
