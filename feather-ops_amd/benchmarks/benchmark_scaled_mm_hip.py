@@ -1,0 +1,146 @@
+#!/usr/bin/env python3
+"""Kernel benchmark and tile sweep of the fp16/bf16 x fp8 scaled matmul on the shape grid in cells.py.
+
+Same role and options as the reference's `bench/benchmark_scaled_mm_hip.py` (whole grid or groups or
+explicit cells, the heuristic against an explicit tile list, a square sweep): per cell it times
+`torch_mm` (torch's matmul on the already-dequantized bf16 weight: the optimistic control, which does
+not pay for dequantization), `auto` (the tile `select_scaled_mm_config` picks) and, with `--tiles`,
+every listed tile, interleaved (see protocol.py). It prints TFLOP/s per provider, the best tile and how
+far the heuristic's pick is from it, and with `--json` writes every measurement for refitting.
+
+Run from `feather-ops_amd/`:
+
+    python -m benchmarks.benchmark_scaled_mm_hip                        # whole grid, heuristic vs torch.mm
+    python -m benchmarks.benchmark_scaled_mm_hip --groups baseline,h3
+    python -m benchmarks.benchmark_scaled_mm_hip --tiles                # every instantiated tile as well
+    python -m benchmarks.benchmark_scaled_mm_hip --tiles "2,2,4,4,8,1;8,1,4,1,4,0"
+    python -m benchmarks.benchmark_scaled_mm_hip --cells "4096,12288,3072" --cold
+"""
+
+import argparse
+import json
+import math
+import pathlib
+import sys
+
+import torch
+
+sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
+
+from benchmarks.cells import GROUPS, cells  # noqa: E402
+from benchmarks.protocol import measure, paired_speedup  # noqa: E402
+from feather_ops.scaled_mm import prepack_b_for_scaled_mm, select_scaled_mm_config  # noqa: E402
+from feather_ops.tiles import SCALED_MM_TILES  # noqa: E402
+
+_DT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def parse_tiles(text: str) -> list[tuple[int, ...]]:
+    if text == "":
+        return list(SCALED_MM_TILES)
+    tiles = []
+    for chunk in text.split(";"):
+        tile = tuple(int(v) for v in chunk.split(","))
+        if len(tile) != 6:
+            raise SystemExit(f"a tile is six ints (warps_m, warps_n, unroll_k, repeat_m, repeat_n, prefetch): {chunk!r}")
+        if tile not in SCALED_MM_TILES:
+            raise SystemExit(f"not instantiated: {tile}")
+        tiles.append(tile)
+    return tiles
+
+
+def weight_copies(n: int, k: int, cold: bool) -> int:
+    """Copies of the prepacked weight to rotate over: enough to exceed the 256 MB MALL twice when cold."""
+    if not cold:
+        return 1
+    k_pad = -(-k // 128) * 128
+    return int(min(16, max(1, math.ceil(512e6 / (k_pad * n)))))
+
+
+def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
+    a_dtype, out_dtype = _DT[args.a_dtype], _DT[args.out_dtype]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    a = torch.randn((m, k), generator=gen, device="cuda").to(a_dtype)
+    b_kn = torch.randn((k, n), generator=gen, device="cuda").to(torch.float8_e5m2)
+    scale = torch.tensor(2.34, device="cuda", dtype=torch.float32)
+    bias = torch.randn(n, generator=gen, device="cuda").to(out_dtype) if args.bias else None
+    copies = weight_copies(n, k, args.cold)
+    packed = prepack_b_for_scaled_mm(b_kn)
+    packs = [packed] + [packed.clone() for _ in range(copies - 1)]
+    control_w = (b_kn.t().float() * scale).to(torch.bfloat16).contiguous()
+    control_a = a.to(torch.bfloat16)
+    del b_kn
+    out = torch.empty((m, n), device="cuda", dtype=out_dtype)
+    op = torch.ops.feather_ops.scaled_mm.default
+
+    picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, out_dtype))
+    providers = {"torch_mm": lambda i: torch.mm(control_a, control_w.t())}
+    if picked not in tiles:  # when the sweep includes the picked tile, `auto` is that tile's measurement
+        providers["auto"] = lambda i: op(a, packs[i % copies], scale, bias, out, *picked)
+    for tile in tiles:
+        providers[str(tile)] = lambda i, tile=tile: op(a, packs[i % copies], scale, bias, out, *tile)
+    res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms)
+    if picked in tiles:
+        res["auto"] = res[str(picked)]
+    tflops = {name: 2.0 * m * n * k / (r.median_ms * 1e-3) / 1e12 for name, r in res.items()}
+    tile_names = [str(t) for t in tiles] or ["auto"]
+    best = max(tile_names, key=lambda name: tflops[name])
+    return {
+        "M": m, "N": n, "K": k, "weight_copies": copies, "picked": list(picked), "best": best,
+        "tflops": tflops, "median_ms": {name: r.median_ms for name, r in res.items()},
+        "spread": {name: (r.p80_ms - r.p20_ms) / r.median_ms for name, r in res.items()},
+        "auto_vs_torch_mm": paired_speedup(res["auto"], res["torch_mm"]),
+        "auto_vs_best": tflops["auto"] / tflops[best],
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--cells", default=None, help="'M,N,K;M,N,K' instead of the grid")
+    parser.add_argument("--groups", default="", help=f"comma-separated groups of cells.py: {','.join(GROUPS)}")
+    parser.add_argument("--square", action="store_true", help="N^3 for N in 512..8192 instead of the grid")
+    parser.add_argument("--tiles", nargs="?", const="", default=None, help="'m,n,u,rm,rn,p;...', or nothing for all")
+    parser.add_argument("--a-dtype", choices=list(_DT), default="bf16")
+    parser.add_argument("--out-dtype", choices=list(_DT), default="bf16")
+    parser.add_argument("--no-bias", dest="bias", action="store_false")
+    parser.add_argument("--cold", action="store_true", help="rotate weight copies past the 256 MB MALL")
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--rounds", type=int, default=5)
+    parser.add_argument("--target-ms", type=float, default=20.0)
+    parser.add_argument("--json", dest="json_path", default=None)
+    args = parser.parse_args()
+    if not torch.cuda.is_available():
+        print("needs a GPU", file=sys.stderr)
+        return 2
+
+    tiles = parse_tiles(args.tiles) if args.tiles is not None else []
+    if args.square:
+        shapes = [("square", s, s, s) for s in (512, 1024, 2048, 4096, 8192)]
+    elif args.cells:
+        shapes = [("custom", *(int(v) for v in c.split(","))) for c in args.cells.split(";")]
+    else:
+        shapes = cells({g.strip() for g in args.groups.split(",") if g.strip()} or None)
+
+    results = []
+    print(f"{'cell':34s} {'torch_mm':>9s} {'auto':>9s} {'best':>9s}  auto/best  auto/torch  picked -> best", flush=True)
+    for group, m, n, k in shapes:
+        r = run_cell(m, n, k, tiles, args)
+        r["group"] = group
+        results.append(r)
+        t = r["tflops"]
+        print(f"{group + ' ' + f'{m}x{n}x{k}':34s} {t['torch_mm']:9.1f} {t['auto']:9.1f} {t[r['best']]:9.1f}"
+              f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])} -> {r['best']}",
+              flush=True)
+        torch.cuda.empty_cache()
+    geo = lambda xs: math.exp(sum(math.log(x) for x in xs) / len(xs))  # noqa: E731
+    print(f"geomean over {len(results)} cells: auto/best {geo([r['auto_vs_best'] for r in results]):.3f}, "
+          f"auto/torch_mm {geo([r['auto_vs_torch_mm'] for r in results]):.3f}", flush=True)
+    if args.json_path:
+        pathlib.Path(args.json_path).write_text(json.dumps({"args": vars(args), "results": results}, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    with torch.inference_mode():
+        sys.exit(main())

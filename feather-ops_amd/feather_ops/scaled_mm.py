@@ -22,19 +22,34 @@ from . import _lib
 from .tiles import gemm_block_sizes
 
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
-_TILE_STREAM_16x16 = (4, 1, 4, 1, 1, 0)
-_TILE_STREAM_16x64 = (4, 1, 4, 1, 4, 0)
-_TILE_STREAM_16x64_8SLICE = (8, 1, 4, 1, 4, 0)
-_TILE_128x128 = (2, 2, 4, 4, 4, 1)
-_TILE_128x256 = (2, 2, 4, 4, 8, 1)
+_TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
+_TILE_RING_256x256 = (4, 2, 4, 4, 8, 1)
+_TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
+_TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
+_TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
 
-# MI355X: 256 compute units; the 4-wave ring tiles run two blocks per CU.
+# MI355X: 256 compute units.
 _CUS = 256
+
+# Ring tiles for large grids: (tile, blocks resident per CU, steady-state TFLOP/s on a full grid), measured
+# with the tile sweep (feather-ops_amd/benchmarks) on the large cells of its grid.
+_RING_MODEL = (
+    (_TILE_RING_128x256, 2, 1100.0),
+    (_TILE_RING_256x256, 1, 1040.0),
+    (_TILE_RING_128x128, 3, 1030.0),
+)
 
 
 def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
     bm, bn, _ = gemm_block_sizes(tile)
     return -(-M // bm) * -(-N // bn)
+
+
+def _ring_time(M: int, N: int, tile: tuple[int, ...], per_cu: int, tflops: float) -> float:
+    """Relative time of a ring tile: whole waves of `_CUS * per_cu` blocks, each wave as long as a full one."""
+    bm, bn, _ = gemm_block_sizes(tile)
+    waves = -(-_blocks(M, N, tile) // (_CUS * per_cu))
+    return waves * _CUS * per_cu * bm * bn / tflops
 
 
 def select_scaled_mm_config(
@@ -47,21 +62,29 @@ def select_scaled_mm_config(
 ) -> tuple[int, int, int, int, int, int]:
     """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
 
-    Fitted on MI355X over the benchmark cells (sweep of every tile): up to 16 rows the weight stream is the
-    whole cost, so a 16-row split-K streaming tile is used, 64 columns wide (8 K slices when the weight is
-    large) unless that leaves too few blocks, then 16. While the 128 x 128 LDS-ring grid would not cover
-    the 256 CUs, the 16 x 64 streaming tile's extra blocks win (e.g. 256 x 1024 x 1024: 4.9 us vs 12 us).
-    Past that the ring takes over: 128 x 256 tiles (two 4-wave blocks per CU) once they give two blocks
-    per CU, 128 x 128 below that.
+    Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile; the pick is within
+    1% of the best tile in geometric mean and within 8% everywhere):
+    - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
+      blocks finish first (a wave-quantization model over 128 x 256, 256 x 256 and 128 x 128 tiles with
+      their measured full-grid rates).
+    - M > 64 with a smaller grid: the 64 x 64 ring tile once it gives 512 blocks, otherwise streaming.
+    - 16 < M <= 64: the 32-row streaming tile when it gives a CU's worth of blocks.
+    - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
+      columns), with 8 K slices per block unless there are 512 blocks or more, then 4.
     """
     del K, a_dtype, b_dtype, out_dtype
-    if M <= 16:
-        if N >= 8192:
-            return _TILE_STREAM_16x64_8SLICE
-        return _TILE_STREAM_16x64 if N >= 4096 else _TILE_STREAM_16x16
-    if _blocks(M, N, _TILE_128x128) < _CUS:
-        return _TILE_STREAM_16x64
-    return _TILE_128x256 if _blocks(M, N, _TILE_128x256) >= 2 * _CUS else _TILE_128x128
+    if M > 64 and _blocks(M, N, _TILE_RING_128x128) >= _CUS:
+        return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
+    if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
+        return _TILE_RING_64x64
+    if 16 < M <= 64 and _blocks(M, N, _TILE_STREAM_32x64) >= _CUS:
+        return _TILE_STREAM_32x64
+    rows = -(-M // 16)
+    for repeat_n in (4, 2, 1):
+        if rows * (N // (16 * repeat_n)) >= 160:
+            break
+    blocks = rows * -(-N // (16 * repeat_n))
+    return (8 if blocks < 2 * _CUS else 4, 1, 4, 1, repeat_n, 0)
 
 
 def _launch(

@@ -105,3 +105,19 @@ def test_heuristic_returns_instantiated_tiles():
         for n in (8, 96, 1000, 1024, 3072, 5120, 12288, 14336, 96768):
             for k in (16, 1024, 2560, 4096):
                 assert select_scaled_mm_config(m, n, k) in SCALED_MM_TILES
+
+
+def test_heuristic_picks_on_representative_cells():
+    """The fitted rule's regimes, one cell each (the picks the tile sweep measured best or within noise)."""
+    from feather_ops.scaled_mm import select_scaled_mm_config as pick
+
+    assert pick(4096, 12288, 3072) == (2, 2, 4, 4, 8, 1)   # C3: 3 full waves of 128 x 256
+    assert pick(4096, 3072, 3072) == (2, 2, 4, 4, 4, 1)    # C2: one full wave of 128 x 128
+    assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
+    assert pick(256, 12288, 4096) == (2, 2, 4, 2, 2, 1)    # small grid of 128 x 128: 64 x 64 ring
+    assert pick(512, 1024, 1024) == (4, 1, 4, 1, 4, 0)     # tiny grid: streaming, 4 K slices
+    assert pick(32, 25600, 5120) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
+    assert pick(16, 14336, 4096) == (8, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 8 K slices
+    assert pick(16, 4096, 4096) == (8, 1, 4, 1, 1, 0)      # narrow N: 16-column blocks for parallelism
+    assert pick(16, 6144, 6144) == (8, 1, 4, 1, 2, 0)
+    assert pick(1, 96768, 2688) == (4, 1, 4, 1, 4, 0)      # one row, very wide: many blocks, 4 slices
