@@ -136,6 +136,37 @@ void bf16_to_fp16(const Tensor& x, Tensor& out) {
     STD_TORCH_CHECK(err == hipSuccess, "bf16_to_fp16 kernel launch failed: ", hipGetErrorString(err));
 }
 
+// feather_ops::prepack_b: out[k // 16, n, k % 16] = b[k, n] for a [K, N] fp8 weight, K zero-padded to a
+// multiple of 128 (the reference's prepack_b_for_scaled_mm layout, feather_ops/scaled_mm.py:137-150).
+void prepack_b(const Tensor& b, Tensor& out) {
+    STD_TORCH_CHECK(b.is_cuda() && out.is_cuda(), "b and out must be CUDA tensors");
+    STD_TORCH_CHECK(b.get_device_index() == out.get_device_index(), "b and out must be on one device");
+    STD_TORCH_CHECK(b.scalar_type() == ST::Float8_e5m2 || b.scalar_type() == ST::Float8_e4m3fn,
+                    "b must be float8_e5m2 or float8_e4m3fn");
+    STD_TORCH_CHECK(out.scalar_type() == b.scalar_type(), "out must have b's dtype");
+    STD_TORCH_CHECK(b.dim() == 2 && out.dim() == 3, "b must be 2-D [K, N] and out 3-D [K_pad/16, N, 16]");
+    STD_TORCH_CHECK(b.is_contiguous() && out.is_contiguous(), "b and out must be contiguous");
+    const int64_t K = b.size(0);
+    const int64_t N = b.size(1);
+    const int64_t k_pad = (K + 127) / 128 * 128;
+    STD_TORCH_CHECK(K >= 1 && N % 8 == 0 && N >= 8, "prepack_b needs K >= 1 and N a positive multiple of 8");
+    STD_TORCH_CHECK(out.size(0) == k_pad / 16 && out.size(1) == N && out.size(2) == 16,
+                    "out must be [ceil(K/128)*8, N, 16]");
+    STD_TORCH_CHECK(k_pad * N < (int64_t{1} << 31), "the prepacked weight must be smaller than 2 GiB");
+    STD_TORCH_CHECK(is_aligned(b.const_data_ptr(), 8) && is_aligned(out.mutable_data_ptr(), 16),
+                    "b must be 8-byte and out 16-byte aligned");
+    const auto device_index = b.get_device_index();
+    torch::stable::accelerator::DeviceGuard guard(device_index);
+    void* raw_stream = nullptr;
+    TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &raw_stream));
+    const bool launched = feather_prepack_b(static_cast<const uint8_t*>(b.const_data_ptr()),
+                                            static_cast<uint8_t*>(out.mutable_data_ptr()), K, N,
+                                            static_cast<hipStream_t>(raw_stream));
+    STD_TORCH_CHECK(launched, "prepack_b: unsupported arguments");
+    const hipError_t err = hipGetLastError();
+    STD_TORCH_CHECK(err == hipSuccess, "prepack_b kernel launch failed: ", hipGetErrorString(err));
+}
+
 }  // namespace
 
 STABLE_TORCH_LIBRARY(feather_ops, m) {
@@ -143,11 +174,13 @@ STABLE_TORCH_LIBRARY(feather_ops, m) {
         "scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, int block_warps_m, "
         "int block_warps_n, int unroll_k, int repeat_m, int repeat_n, bool prefetch) -> ()");
     m.def("bf16_to_fp16(Tensor x, Tensor(a!) out) -> ()");
+    m.def("prepack_b(Tensor b, Tensor(a!) out) -> ()");
 }
 
 STABLE_TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm", TORCH_BOX(&scaled_mm));
     m.impl("bf16_to_fp16", TORCH_BOX(&bf16_to_fp16));
+    m.impl("prepack_b", TORCH_BOX(&prepack_b));
 }
 
 extern "C" PyObject* PyInit__C(void) {

@@ -136,11 +136,17 @@ def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
     """`[K, N]` fp8 -> `[K_pad/16, N, 16]`, the layout the kernel indexes (reference `scaled_mm.py:137-150`).
 
     `K` is zero-padded to a multiple of 128, so a ragged K never needs a staging branch; element
-    `[k // 16, n, k % 16]` of the result is `b[k, n]`. Runs as torch copy kernels on `b`'s device, once
-    per weight.
+    `[k // 16, n, k % 16]` of the result is `b[k, n]`. A contiguous e5m2 / e4m3fn weight on the GPU with
+    N a multiple of 8 is permuted by one HIP kernel (`csrc/prepack.hip`, HBM-bound); anything else
+    (a CPU weight, another dtype or width) by torch copy kernels on `b`'s device. Run once per weight.
     """
     k, n = b.shape
     k_pad = -(-k // 128) * 128
+    if (b.is_cuda and b.dtype in (torch.float8_e5m2, torch.float8_e4m3fn) and b.is_contiguous()
+            and n % 8 == 0 and n > 0 and k > 0 and b.data_ptr() % 8 == 0):
+        out = torch.empty((k_pad // 16, n, 16), device=b.device, dtype=b.dtype)
+        torch.ops.feather_ops.prepack_b.default(b, out)
+        return out
     if k_pad != k:
         padded = torch.zeros((k_pad, n), device=b.device, dtype=b.dtype)
         padded[:k] = b

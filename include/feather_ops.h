@@ -52,6 +52,16 @@ bool launch_scaled_mm(const uint16_t* a, const uint8_t* b_prepacked, const float
  */
 bool feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
 
+/*
+ * b_prepacked[k / 16][n][k % 16] = b[k][n] for a [K, N] row-major fp8 weight b (the GEMM's B = W^T),
+ * with the K_pad - K rows past K (K_pad = ceil(K / 128) * 128) written as zeros: the layout
+ * launch_scaled_mm reads, produced on the GPU and enqueued on `stream`. Restates the reference's Python
+ * prepack_b_for_scaled_mm (feather_ops/scaled_mm.py:137-150), which has no C entry point of its own.
+ * Requires K >= 1, N >= 8 and N % 8 == 0, b 8-byte and b_prepacked 16-byte aligned, K_pad * N < 2^31;
+ * returns false (nothing enqueued) otherwise. b_prepacked holds K_pad / 16 * N * 16 bytes.
+ */
+bool feather_prepack_b(const uint8_t* b, uint8_t* b_prepacked, int64_t K, int64_t N, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,12 +31,15 @@ def lib():
         [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_void_p]
     handle.feather_bf16_to_fp16.restype = ctypes.c_bool
     handle.feather_bf16_to_fp16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    handle.feather_prepack_b.restype = ctypes.c_bool
+    handle.feather_prepack_b.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_void_p]
     return handle
 
 
 def test_library_exports_every_declared_symbol(lib):
     names = _declared()
-    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16"}
+    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_prepack_b"}
     for name in names:
         assert hasattr(lib, name), name
 
@@ -76,6 +79,33 @@ def test_convert_c_abi_refuses_bad_arguments(lib):
     assert lib.feather_bf16_to_fp16(A, C, 0, None) is True  # nothing to do, nothing enqueued
 
 
+@pytest.mark.parametrize("args", [
+    (B, C, 0, 64),            # K < 1
+    (B, C, 128, 12),          # N % 8 != 0
+    (B, C, 128, 0),
+    (B + 4, C, 128, 64),      # b not 8-byte aligned
+    (B, C + 8, 128, 64),      # b_prepacked not 16-byte aligned
+    (None, C, 128, 64),
+    (B, None, 128, 64),
+    (B, C, 1 << 20, 1 << 12),  # prepacked weight 4 GiB
+])
+def test_prepack_c_abi_refuses_bad_arguments(lib, args):
+    assert lib.feather_prepack_b(*args, None) is False
+
+
+def test_prepack_falls_back_to_torch_permutation_off_gpu():
+    """On CPU (and for shapes the kernel does not take) prepack is torch's own permutation of `b`."""
+    from feather_ops import prepack_b_for_scaled_mm
+
+    b = torch.arange(200 * 24, dtype=torch.int32).remainder(256).to(torch.uint8).view(200, 24)
+    p = prepack_b_for_scaled_mm(b.view(torch.float8_e5m2)).view(torch.uint8)
+    assert p.shape == (16, 24, 16)
+    k = torch.arange(256).view(-1, 1)
+    want = torch.zeros(256, 24, dtype=torch.uint8)
+    want[:200] = b
+    assert torch.equal(p[k // 16, torch.arange(24).view(1, -1), k % 16], want)
+
+
 def test_torch_ops_are_registered_for_the_gpu_only():
     import feather_ops  # noqa: F401
 
@@ -86,6 +116,9 @@ def test_torch_ops_are_registered_for_the_gpu_only():
         torch.ops.feather_ops.scaled_mm.default(a, b, None, None, c, 2, 2, 4, 4, 4, True)
     with pytest.raises((NotImplementedError, RuntimeError)):
         torch.ops.feather_ops.bf16_to_fp16.default(torch.zeros(8, dtype=torch.bfloat16), torch.empty(8, dtype=torch.float16))
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.feather_ops.prepack_b.default(torch.zeros(16, 8, dtype=torch.float8_e5m2),
+                                                torch.empty(8, 8, 16, dtype=torch.float8_e5m2))
 
 
 def test_scaled_mm_hip_has_no_cpu_fallback():
