@@ -35,7 +35,7 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile without a
 # measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
-    ("c3", (2, 2, 4, 4, 8, 1)): (192487 * 2.0 + 101899 * 1.0) * 1024,
+    ("c3", (2, 2, 4, 4, 8, 1)): (192379 * 2.0 + 101770 * 1.0) * 1024,
     ("c4", (8, 1, 4, 1, 4, 0)): (29219 * 2.0 + 448 * 1.0) * 1024,
 }
 
@@ -133,6 +133,31 @@ def time_c4(reps: int = 50, copies: int = 8):
             "bytes": nbytes, "weight_copies": copies}
 
 
+def time_c2(steps: int = 100, warmup: int = 10):
+    """C2, the bf16-activation cell (bf16 [4096, 3072] x e5m2 [3072, 3072] -> bf16), TFLOP/s."""
+    import torch
+
+    import feather_ops
+
+    m, k, n = 4096, 3072, 3072
+    a, bs, s = make_device_inputs(m, k, n, "bf16")
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.bfloat16)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    op = torch.ops.feather_ops.scaled_mm.default
+    for _ in range(warmup):
+        op(a, bs[0], s, None, out, *tile)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        op(a, bs[0], s, None, out, *tile)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+
+
 def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     """One kernel, `warmup + steps` eager launches, nothing else: the target of rocprofv3 --pmc runs.
 
@@ -162,7 +187,7 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     torch.cuda.synchronize()
 
 
-def time_cpu_oracle(budget_s: float = 10.0):
+def time_cpu_oracle(budget_s: float = 20.0):
     """The oracle on host cores over a row sample of the C3 workload (the same device-generated inputs,
     copied to the host), scaled to TFLOP/s. The oracle is the checker; it is only timed here."""
     import numpy as np
@@ -201,7 +226,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 HBM measurement")
+    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 (HBM) and C2 (bf16) cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()
@@ -222,6 +247,7 @@ def main() -> int:
         return 0
     c3 = time_c3(args.steps, args.warmup)
     c4 = None if args.no_secondary else time_c4()
+    c2 = None if args.no_secondary else time_c2()
     cpu = None if args.no_cpu else time_cpu_oracle()
 
     line = {
@@ -250,6 +276,10 @@ def main() -> int:
                             "frac_hbm_peak": round(c4["gbps"] / PEAK_HBM_GBPS, 4), "tile": c4["tile"],
                             "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"],
                             "traffic": MEASURED_TRAFFIC_BYTES.get(("c4", tuple(c4["tile"])))}
+    if c2 is not None:
+        line["bf16_cell"] = {"workload": "C2 DiT attention projection: bf16 [4096,3072] x e5m2 [3072,3072] -> bf16",
+                             "TFLOPs": round(c2["tflops"], 1), "us_per_launch": round(c2["us"], 2),
+                             "frac_fp16_peak": round(c2["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": c2["tile"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))
