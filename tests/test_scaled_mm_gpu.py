@@ -129,6 +129,36 @@ def test_heuristic_matches_a_measured_tile(fo):
     check_against_oracle(out, a, bp, scale, None, rows=sample_rows(4112))
 
 
+# One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, the
+# 32-row streaming tile, the 64 x 64 ring tile for mid-size grids, and the wave-quantization choice among
+# 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out with a bias, against the oracle.
+HEURISTIC_CELLS = [
+    (2, 4096, 16384),    # 16 x 16 columns, 8 slices
+    (16, 6144, 6144),    # 16 x 32 columns
+    (32, 25600, 5120),   # 32-row streaming tile
+    (128, 1024, 5120),   # 16-row tile, 8 row blocks
+    (256, 12288, 4096),  # 64 x 64 ring tile
+    (512, 1024, 1024),   # 4-slice streaming tile
+    (9216, 2048, 2048),  # 128 x 128 (one full wave of blocks)
+    (2320, 6144, 6144),  # 128 x 256
+]
+
+
+@pytest.mark.parametrize("m,n,k", HEURISTIC_CELLS)
+def test_heuristic_regimes(fo, m, n, k):
+    from feather_ops.scaled_mm import select_scaled_mm_config
+
+    a = _tensor((m, k), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
+    scale = torch.tensor(0.75, device="cuda", dtype=torch.float32)
+    bias = _tensor((n,), torch.bfloat16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16)
+    tile = select_scaled_mm_config(m, n, k, torch.bfloat16, torch.float8_e5m2, torch.bfloat16)
+    rows = None if m * n * k <= (1 << 28) else sample_rows(m, n_random=16)
+    res = check_against_oracle(out, a, bp, scale, bias, rows=rows)
+    print(f"{m}x{n}x{k} tile {tile}: max_abs={res['max_abs']:.4g} bound={res['bound']:.4g}")
+
+
 # ---- BASELINE configurations (north-star recipe) -----------------------------------------------------------
 
 CONFIGS = {
