@@ -25,7 +25,8 @@ bool is_aligned(const void* p, uintptr_t bytes) {
 }
 
 // feather_ops::scaled_mm. Preconditions and messages follow csrc/hip_kernel.cu:729-801; N is relaxed from
-// a multiple of 16 to a multiple of 8 (16-byte output rows stay aligned, partial 16-column tiles are masked).
+// a multiple of 16 to a multiple of 8 (16-byte output rows stay aligned, partial 16-column tiles are masked),
+// and scale may also hold one value per output column (the per-channel scale of feather_ops/naive.py:29-33).
 void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
                const std::optional<Tensor>& bias, Tensor& c, const int64_t block_warps_m, const int64_t block_warps_n,
                const int64_t unroll_k, const int64_t repeat_m, const int64_t repeat_n, const bool prefetch) {
@@ -72,8 +73,16 @@ void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<T
         STD_TORCH_CHECK(s.is_cuda(), "scale must be a CUDA tensor");
         STD_TORCH_CHECK(s.get_device_index() == device_index, "scale must be on the same device as a");
         STD_TORCH_CHECK(s.scalar_type() == ST::Float, "scale must be float32");
-        STD_TORCH_CHECK(s.numel() == 1, "scale must have one element");
+        STD_TORCH_CHECK(s.numel() == 1 || s.numel() == N,
+                        "scale must have one element (per tensor) or N elements (per output column)");
+        if (s.numel() == N) {
+            STD_TORCH_CHECK(s.dim() == 1, "a per-column scale must be 1D");
+            STD_TORCH_CHECK(s.stride(0) == 1, "a per-column scale must be contiguous");
+            STD_TORCH_CHECK(is_aligned(s.const_data_ptr(), 16), "a per-column scale must be 16-byte aligned");
+        }
     }
+    // 1: one per-tensor value; 2: one value per output column (N >= 8, so the two never coincide).
+    const int scale_mode = !scale.has_value() ? 0 : scale->numel() == 1 ? 1 : 2;
     if (bias.has_value()) {
         const Tensor& b = *bias;
         STD_TORCH_CHECK(b.is_cuda(), "bias must be a CUDA tensor");
@@ -103,7 +112,7 @@ void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<T
         static_cast<const uint16_t*>(a.const_data_ptr()), static_cast<const uint8_t*>(b_prepacked.const_data_ptr()),
         scale.has_value() ? static_cast<const float*>(scale->const_data_ptr()) : nullptr,
         bias.has_value() ? static_cast<const uint16_t*>(bias->const_data_ptr()) : nullptr,
-        static_cast<uint16_t*>(c.mutable_data_ptr()), M, N, K, scale.has_value() ? 1 : 0, bias.has_value() ? 1 : 0,
+        static_cast<uint16_t*>(c.mutable_data_ptr()), M, N, K, scale_mode, bias.has_value() ? 1 : 0,
         b_type == ST::Float8_e5m2, a_type == ST::BFloat16, c.scalar_type() == ST::BFloat16,
         static_cast<int>(block_warps_m), static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
         static_cast<int>(repeat_m), static_cast<int>(repeat_n), prefetch, static_cast<hipStream_t>(raw_stream));

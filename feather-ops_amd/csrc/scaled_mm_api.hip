@@ -23,6 +23,7 @@ bool contract_ok(const uint16_t* a, const uint8_t* b, const float* scale, const 
     if (has_bias && !bias) return false;
     if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16)) return false;
     if (has_bias && !aligned(bias, 8)) return false;
+    if (has_scale == 2 && !aligned(scale, 16)) return false;
     const int64_t kb_rows = (K + 127) / 128 * 8;
     if (M * K * 2 > kMaxBufferBytes || M * N * 2 > kMaxBufferBytes || kb_rows * N * 16 > kMaxBufferBytes) {
         return false;
@@ -45,6 +46,7 @@ extern "C" bool launch_scaled_mm(const uint16_t* const a, const uint8_t* const b
     p.a = a;
     p.b = b_prepacked;
     p.scale = has_scale ? scale : nullptr;
+    p.col_scale = has_scale == 2 ? 1 : 0;
     p.bias = has_bias ? bias : nullptr;
     p.c = c;
     p.M = static_cast<int32_t>(M);

@@ -54,11 +54,12 @@ constexpr int kRsrcFlags = 0x00020000;
 struct Params {
     const uint16_t* a;          // [M, K] fp16 or bf16 bits, row-major
     const uint8_t* b;           // [kb_total, N, 16] fp8 codes
-    const float* scale;         // 1 fp32 value, or nullptr
+    const float* scale;         // 1 fp32 value (col_scale == 0) or N (col_scale != 0), or nullptr
     const uint16_t* bias;       // [N] in the output dtype, or nullptr
     uint16_t* c;                // [M, N] output bits, row-major
     int32_t M, N, K;
     int32_t kb_total;           // b_prepacked.shape[0]
+    int32_t col_scale;          // scale holds one value per output column (16-byte aligned)
 };
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -168,12 +169,13 @@ __device__ __forceinline__ float out_to_f32(uint32_t bits) {
 }
 
 // acc (4 consecutive columns of one row) -> scaled, rounded, biased output bits, packed for one 8-byte store.
+// scale: the 4 columns' scales (all equal for a per-tensor scale).
 template <bool kOutBf16>
-__device__ __forceinline__ u32x2 epilogue4(const f32x4 acc, float scale, bool has_bias, u32x2 bias_bits) {
+__device__ __forceinline__ u32x2 epilogue4(const f32x4 acc, f32x4 scale, bool has_bias, u32x2 bias_bits) {
     uint32_t o[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        uint32_t y = round_out<kOutBf16>(acc[v] * scale);
+        uint32_t y = round_out<kOutBf16>(acc[v] * scale[v]);
         if (has_bias) {
             const uint32_t bb = (bias_bits[v / 2] >> (16 * (v % 2))) & 0xffffu;
             y = round_out<kOutBf16>(out_to_f32<kOutBf16>(y) + out_to_f32<kOutBf16>(bb));
@@ -187,9 +189,34 @@ __device__ __forceinline__ f32x4 mfma16(half8 w, half8 x, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(w, x, acc, 0, 0, 0);
 }
 
-// The per-tensor weight scale, read once at kernel start so that its latency hides under the main loop.
+// The per-tensor weight scale, read once at kernel start so that its latency hides under the main loop
+// (1 when there is none or the scales are per column).
 __device__ __forceinline__ float load_scale(const Params& p) {
-    return p.scale ? *p.scale : 1.0f;
+    return p.scale && !p.col_scale ? *p.scale : 1.0f;
+}
+
+// Per-column scales of the 4 columns each lane stores in each of a wave's RN column tiles (16-byte loads:
+// the 4 columns start at a multiple of 4), issued together. Columns past N read 0; they are not stored.
+template <int RN>
+__device__ __forceinline__ void load_col_scales(const Params& p, int col0, int lane, f32x4 (&scales)[RN]) {
+    const int c_in = 4 * (lane >> 4);
+    const rsrc_t scale_rsrc = make_rsrc(p.scale, static_cast<uint32_t>(p.N) * 4u);
+#pragma unroll
+    for (int j = 0; j < RN; ++j) {
+        const int col = col0 + 16 * j + c_in;
+        const uint32_t off = col < p.N ? static_cast<uint32_t>(col) * 4u : kOob;
+        scales[j] = __builtin_bit_cast(f32x4, buf_load16(scale_rsrc, off));
+    }
+}
+
+// The scale operand of store_tiles: one per-tensor value, or RN vectors of per-column values.
+__device__ __forceinline__ f32x4 tile_scale(float scale, int) {
+    return f32x4{scale, scale, scale, scale};
+}
+
+template <int RN>
+__device__ __forceinline__ f32x4 tile_scale(const f32x4 (&scales)[RN], int j) {
+    return scales[j];
 }
 
 // Bias bits of the 4 columns each lane stores in each of a wave's RN column tiles, all loads issued
@@ -211,9 +238,10 @@ __device__ __forceinline__ void load_bias(const Params& p, int col0, int lane, u
 }
 
 // Store one wave's RM x RN accumulator tiles. rows0/cols0: the wave's first output row and column.
-template <int RM, int RN, bool kOutBf16>
+// scale: a float (per tensor) or f32x4[RN] (per column, from load_col_scales).
+template <int RM, int RN, bool kOutBf16, typename Scale>
 __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[RM][RN], int row0, int col0,
-                                            int lane, float scale, const u32x2 (&bias_bits)[RN]) {
+                                            int lane, const Scale& scale, const u32x2 (&bias_bits)[RN]) {
     const rsrc_t c_rsrc = make_rsrc(p.c, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.N) * 2u);
     const bool has_bias = p.bias != nullptr;
     const int r_in = lane & 15;
@@ -229,8 +257,25 @@ __device__ __forceinline__ void store_tiles(const Params& p, const f32x4 (&acc)[
             const uint32_t off = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.N) +
                                        static_cast<uint32_t>(col)) * 2u
                                     : kOob;
-            buf_store8(epilogue4<kOutBf16>(acc[i][j], scale, has_bias, bias_bits[j]), c_rsrc, off);
+            buf_store8(epilogue4<kOutBf16>(acc[i][j], tile_scale(scale, j), has_bias, bias_bits[j]), c_rsrc, off);
         }
+    }
+}
+
+// A wave's whole epilogue: bias (and per-column scale) loads for its RN column tiles, all in flight
+// together, then the RM x RN stores. The scale mode is uniform, so each branch is a straight-line store
+// sequence and the per-tensor one holds no scale vectors.
+template <int RM, int RN, bool kOutBf16>
+__device__ __forceinline__ void store_wave_tiles(const Params& p, const f32x4 (&acc)[RM][RN], int row0, int col0,
+                                                 int lane, float scale) {
+    u32x2 bias_bits[RN];
+    load_bias<RN>(p, col0, lane, bias_bits);
+    if (p.col_scale) {
+        f32x4 col_scales[RN];
+        load_col_scales<RN>(p, col0, lane, col_scales);
+        store_tiles<RM, RN, kOutBf16>(p, acc, row0, col0, lane, col_scales, bias_bits);
+    } else {
+        store_tiles<RM, RN, kOutBf16>(p, acc, row0, col0, lane, scale, bias_bits);
     }
 }
 
@@ -585,9 +630,7 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
         }
     }
 
-    u32x2 bias_bits[RN];
-    load_bias<RN>(p, n0 + wave_n * 16 * RN, lane, bias_bits);
-    store_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale, bias_bits);
+    store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale);
 }
 
 // ---- stream kernel: split-K, global -> VGPR ----------------------------------------------------------------
@@ -789,15 +832,19 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             const int col0 = tn * S::kBN + (f / (RM * RN)) * 16 * RN + 16 * j;
             u32x2 bias_bits[1];
             load_bias<1>(p, col0, lane, bias_bits);
+            f32x4 col_scales[1];
+            if (p.col_scale) load_col_scales<1>(p, col0, lane, col_scales);
             f32x4 sum[1][1] = {{red[f * kWave + lane]}};
 #pragma unroll
             for (int k2 = 1; k2 < KS; ++k2) sum[0][0] += red[(k2 * S::kFrags + f) * kWave + lane];
-            store_tiles<1, 1, kOutBf16>(p, sum, m0 + 16 * i, col0, lane, scale, bias_bits);
+            if (p.col_scale) {
+                store_tiles<1, 1, kOutBf16>(p, sum, m0 + 16 * i, col0, lane, col_scales, bias_bits);
+            } else {
+                store_tiles<1, 1, kOutBf16>(p, sum, m0 + 16 * i, col0, lane, scale, bias_bits);
+            }
         }
     } else {
-        u32x2 bias_bits[RN];
-        load_bias<RN>(p, n0, lane, bias_bits);
-        store_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane, scale, bias_bits);
+        store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane, scale);
     }
 }
 

@@ -2,9 +2,10 @@
 
 Drop-in for the reference's `feather_ops/scaled_mm.py` (same names, arguments and op boundary):
 `X` is fp16 or bf16 `[M, K]`, `W` is fp8e5m2 or fp8e4m3fn stored as `[K_pad/16, N, 16]` (see
-`prepack_b_for_scaled_mm`), `scale` is a per-tensor fp32 scalar on the device and `bias` is optional. The
-output is fp16 or bf16. Any `M >= 1` works, with `K` a multiple of 16 and `N` a multiple of 8 (the
-reference needs 16).
+`prepack_b_for_scaled_mm`), `scale` is a per-tensor fp32 scalar on the device (or, beyond the
+reference kernel, N fp32 values, one per output column, as the reference's naive path accepts with
+`bias_dim=1`, `naive.py:29-33`) and `bias` is optional. The output is fp16 or bf16. Any `M >= 1` works,
+with `K` a multiple of 16 and `N` a multiple of 8 (the reference needs 16).
 
 Numerics are the naive path's (`feather_ops/naive.py:4-41`) with fp32 accumulation: bf16 activations are
 widened to fp16 (RNE), the weight decodes exactly to fp16, the MFMAs accumulate in fp32, the scale is

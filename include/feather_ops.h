@@ -26,7 +26,10 @@ typedef struct ihipStream_t* hipStream_t;
  *                widened to fp16 with round-to-nearest-even, as feather_ops/naive.py:21 does.
  *   b_prepacked  [K_pad/16, N, 16] fp8 codes, e5m2 (use_fp8_e5m2 = true) or e4m3fn (false), K_pad a
  *                multiple of 128 with zero pad rows (feather_ops/scaled_mm.py:137-150).
- *   scale        one fp32 value in device memory, read by the kernel (has_scale != 0), or ignored.
+ *   scale        fp32 in device memory, read by the kernel: one per-tensor value (has_scale == 1, or any
+ *                non-zero value other than 2), N per-output-column values (has_scale == 2, 16-byte aligned;
+ *                an extension: the reference kernel takes only the per-tensor form, its naive path
+ *                feather_ops/naive.py:29-33 both), or ignored (has_scale == 0).
  *   bias         N values of the output dtype (has_bias != 0), added after the downcast, or ignored.
  *   c            [M, N] row-major output, fp16 (output_bf16 = false) or bf16 (true), rounded to nearest even.
  *   tile         (block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch): one entry of

@@ -21,7 +21,10 @@ What pins each function (tests/test_oracle.py):
 - `scaled_mm` (C `oracle_scaled_mm`): closed forms (identity weight, one non-zero, zero activations,
   power-of-two scales), brute-force float64 loops on tiny inputs, and golden fixtures computed by float64
   `numpy.matmul` on the decoded operands (`tests/golden/make_golden.py`), chosen non-square and
-  non-symmetric so that a transposed operand, a dropped k term or a wrong scale/bias order fails.
+  non-symmetric so that a transposed operand, a dropped k term or a wrong scale/bias order fails. The
+  per-output-column scale (`naive.py:29-33`) is pinned by distinct power-of-two column scales (exact:
+  column n equals the unscaled column times scale[n], so a row/column mix-up fails), by a constant vector
+  agreeing bit for bit with the per-tensor scale, and by float64 loops on tiny inputs.
 - `scaled_mm_band`: the same core as `scaled_mm` evaluated at the fp32 value -/+ delta; pinned by the
   answer at delta = 0 (itself pinned by the goldens) and by monotonicity (lo <= answer <= hi) on a
   seeded bf16 cell.
@@ -67,19 +70,19 @@ def _load():
         i64 = ctypes.c_int64
         lib.oracle_scaled_mm.argtypes = [
             u16p, ctypes.c_int, u8p, ctypes.c_int, i64, i64, i64,
-            ctypes.POINTER(ctypes.c_float), u16p, ctypes.c_int, u16p,
+            ctypes.POINTER(ctypes.c_float), i64, u16p, ctypes.c_int, u16p,
             ctypes.POINTER(ctypes.c_int64), i64, ctypes.c_int,
         ]
         lib.oracle_scaled_mm.restype = None
         lib.oracle_scaled_mm_f32.argtypes = [
             u16p, ctypes.c_int, u8p, ctypes.c_int, i64, i64, i64,
-            ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+            ctypes.POINTER(ctypes.c_float), i64, ctypes.POINTER(ctypes.c_float),
             ctypes.POINTER(ctypes.c_int64), i64, ctypes.c_int,
         ]
         lib.oracle_scaled_mm_f32.restype = None
         lib.oracle_scaled_mm_band.argtypes = [
             u16p, ctypes.c_int, u8p, ctypes.c_int, i64, i64, i64,
-            ctypes.POINTER(ctypes.c_float), u16p, ctypes.c_int, ctypes.c_float, u16p, u16p,
+            ctypes.POINTER(ctypes.c_float), i64, u16p, ctypes.c_int, ctypes.c_float, u16p, u16p,
             ctypes.POINTER(ctypes.c_int64), i64, ctypes.c_int,
         ]
         lib.oracle_scaled_mm_band.restype = None
@@ -165,13 +168,23 @@ def unpack(packed: np.ndarray, k: int) -> np.ndarray:
 
 # ---- the matmul ------------------------------------------------------------------------------------------
 
-def scaled_mm(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale: float | None,
+def _scales(scale, n: int) -> np.ndarray | None:
+    """None, a python float (one per-tensor fp32 value) or N per-output-column values -> fp32 array."""
+    if scale is None:
+        return None
+    sc = np.ascontiguousarray(np.atleast_1d(np.asarray(scale, dtype=np.float32)).ravel())
+    assert sc.shape in ((1,), (n,)), f"scale must hold 1 or N={n} values, got {sc.shape}"
+    return sc
+
+
+def scaled_mm(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale,
               bias_bits: np.ndarray | None, out_fmt: str, rows: np.ndarray | None = None,
               threads: int = 0) -> np.ndarray:
     """`naive.py` semantics with fp32 accumulation; returns out-dtype bits [M or len(rows), N].
 
     a_bits: [M, K] uint16 (fp16 or bf16 bits). packed: [K_pad/16, N, 16] uint8 codes.
-    scale: python float (rounded to fp32) or None. bias_bits: [N] uint16 in the output format or None.
+    scale: python float (rounded to fp32), N per-output-column values (`naive.py:29-33`, bias_dim = 1) or
+    None. bias_bits: [N] uint16 in the output format or None.
     rows: optional row subset (int64) to evaluate, for full-size spot checks.
     """
     a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
@@ -179,7 +192,7 @@ def scaled_mm(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, sc
     m, k = a_bits.shape
     kb, n, _ = packed.shape
     assert kb * 16 >= k
-    sc = None if scale is None else np.array([scale], dtype=np.float32)
+    sc = _scales(scale, n)
     bias = None if bias_bits is None else np.ascontiguousarray(bias_bits, dtype=np.uint16)
     if bias is not None:
         assert bias.shape == (n,)
@@ -188,33 +201,34 @@ def scaled_mm(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, sc
     out = np.empty((r, n), dtype=np.uint16)
     _load().oracle_scaled_mm(
         _ptr(a_bits, ctypes.c_uint16), int(a_fmt == BF16), _ptr(packed, ctypes.c_uint8), int(b_fmt == E5M2),
-        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float),
+        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float), 0 if sc is None else sc.size,
         None if bias is None else _ptr(bias, ctypes.c_uint16), int(out_fmt == BF16), _ptr(out, ctypes.c_uint16),
         None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),
     )
     return out
 
 
-def scaled_mm_f32(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale: float | None,
+def scaled_mm_f32(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale,
                   rows: np.ndarray | None = None, threads: int = 0) -> np.ndarray:
     """The fp32 value before the output rounding (diagnostics for rounding-neighbour flips)."""
     a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     m, k = a_bits.shape
     _, n, _ = packed.shape
-    sc = None if scale is None else np.array([scale], dtype=np.float32)
+    sc = _scales(scale, n)
     rws = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
     r = m if rws is None else len(rws)
     out = np.empty((r, n), dtype=np.float32)
     _load().oracle_scaled_mm_f32(
         _ptr(a_bits, ctypes.c_uint16), int(a_fmt == BF16), _ptr(packed, ctypes.c_uint8), int(b_fmt == E5M2),
-        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float), _ptr(out, ctypes.c_float),
+        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float), 0 if sc is None else sc.size,
+        _ptr(out, ctypes.c_float),
         None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),
     )
     return out
 
 
-def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale: float | None,
+def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: str, scale,
                    bias_bits: np.ndarray | None, out_fmt: str, delta: float, rows: np.ndarray | None = None,
                    threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
     """The oracle's answers had the fp32 pre-rounding value been `delta` lower / higher (output units).
@@ -227,7 +241,7 @@ def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: st
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     m, k = a_bits.shape
     _, n, _ = packed.shape
-    sc = None if scale is None else np.array([scale], dtype=np.float32)
+    sc = _scales(scale, n)
     bias = None if bias_bits is None else np.ascontiguousarray(bias_bits, dtype=np.uint16)
     rws = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
     r = m if rws is None else len(rws)
@@ -235,7 +249,7 @@ def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: st
     hi = np.empty((r, n), dtype=np.uint16)
     _load().oracle_scaled_mm_band(
         _ptr(a_bits, ctypes.c_uint16), int(a_fmt == BF16), _ptr(packed, ctypes.c_uint8), int(b_fmt == E5M2),
-        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float),
+        m, n, k, None if sc is None else _ptr(sc, ctypes.c_float), 0 if sc is None else sc.size,
         None if bias is None else _ptr(bias, ctypes.c_uint16), int(out_fmt == BF16), float(delta),
         _ptr(lo, ctypes.c_uint16), _ptr(hi, ctypes.c_uint16),
         None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),

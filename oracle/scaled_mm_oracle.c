@@ -9,7 +9,8 @@
  *   feather_ops/naive.py:13-16  unpack the (K_pad/16, N, 16) prepack back to B[K, N]
  *   feather_ops/naive.py:20-22  a.to(fp16), b.to(fp16)        -> widen_a(), decode_b()
  *   feather_ops/naive.py:23     a @ b                          -> exact sum (double), rounded once to fp32
- *   feather_ops/naive.py:24-33  .to(fp32) * scale (per-tensor) -> fp32 multiply
+ *   feather_ops/naive.py:24-33  .to(fp32) * scale             -> fp32 multiply (per tensor, or per output
+ *                                                                  column: bias_dim = 1's scale[None, :])
  *   feather_ops/naive.py:34     .to(out_dtype)                 -> round-to-nearest-even
  *   feather_ops/naive.py:35-40  c += bias (in out precision)   -> fp32 add of two out-dtype values, RNE
  * The literal naive.py accumulates in fp16 and overflows at the per-tensor quantization used here, so the
@@ -167,12 +168,13 @@ static uint16_t finish(float y, const uint16_t* bias, int64_t n, int out_bf16) {
  *
  * a_bf16:  a holds bf16 bits, widened to fp16 with RNE first (naive.py:21 a.to(fp16)); else fp16 bits.
  * b_e5m2:  packed holds e5m2 codes; else e4m3fn codes.
- * scale:   one fp32 value or NULL (no scale step: naive.py:24 skipped).
+ * scale:   scale_n fp32 values (1: per tensor, N: per output column, naive.py:27-33 with bias_dim = 1) or
+ *          NULL (no scale step: naive.py:24 skipped).
  * bias:    N values in the output dtype or NULL.
  * rows:    optional list of n_rows row indices to compute (NULL = all M rows); outputs are [n_rows, N].
  */
 static void core(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N, int64_t K,
-                 const float* scale, const uint16_t* bias, int out_bf16, uint16_t* out, float* out_f32, float delta,
+                 const float* scale, int64_t scale_n, const uint16_t* bias, int out_bf16, uint16_t* out, float* out_f32, float delta,
                  uint16_t* lo, uint16_t* hi, const int64_t* rows, int64_t n_rows, int n_threads) {
     const int64_t R = rows ? n_rows : M;
     float lut[256];
@@ -215,7 +217,7 @@ static void core(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m
                 }
                 float y = (float)acc;
                 if (scale) {
-                    y = y * *scale;
+                    y = y * scale[scale_n == 1 ? 0 : n];
                 }
                 if (out) {
                     out[r * N + n] = finish(y, bias, n, out_bf16);
@@ -237,24 +239,25 @@ static void core(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m
 }
 
 void oracle_scaled_mm(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
-                      int64_t K, const float* scale, const uint16_t* bias, int out_bf16, uint16_t* out,
-                      const int64_t* rows, int64_t n_rows, int n_threads) {
-    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, bias, out_bf16, out, NULL, 0.0f, NULL, NULL, rows, n_rows,
+                      int64_t K, const float* scale, int64_t scale_n, const uint16_t* bias, int out_bf16,
+                      uint16_t* out, const int64_t* rows, int64_t n_rows, int n_threads) {
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, scale_n, bias, out_bf16, out, NULL, 0.0f, NULL, NULL, rows, n_rows,
          n_threads);
 }
 
 /* The fp32 value before the output rounding, for diagnostics: out[r, n] = fp32(sum) (* scale). */
 void oracle_scaled_mm_f32(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
-                          int64_t K, const float* scale, float* out, const int64_t* rows, int64_t n_rows,
-                          int n_threads) {
-    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, NULL, 0, NULL, out, 0.0f, NULL, NULL, rows, n_rows, n_threads);
+                          int64_t K, const float* scale, int64_t scale_n, float* out, const int64_t* rows,
+                          int64_t n_rows, int n_threads) {
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, scale_n, NULL, 0, NULL, out, 0.0f, NULL, NULL, rows, n_rows, n_threads);
 }
 
 /* The answers for a pre-rounding value off by -delta / +delta (absolute, output units). */
 void oracle_scaled_mm_band(const uint16_t* a, int a_bf16, const uint8_t* packed, int b_e5m2, int64_t M, int64_t N,
-                           int64_t K, const float* scale, const uint16_t* bias, int out_bf16, float delta,
-                           uint16_t* lo, uint16_t* hi, const int64_t* rows, int64_t n_rows, int n_threads) {
-    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, bias, out_bf16, NULL, NULL, delta, lo, hi, rows, n_rows,
+                           int64_t K, const float* scale, int64_t scale_n, const uint16_t* bias, int out_bf16,
+                           float delta, uint16_t* lo, uint16_t* hi, const int64_t* rows, int64_t n_rows,
+                           int n_threads) {
+    core(a, a_bf16, packed, b_e5m2, M, N, K, scale, scale_n, bias, out_bf16, NULL, NULL, delta, lo, hi, rows, n_rows,
          n_threads);
 }
 

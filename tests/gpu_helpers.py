@@ -31,11 +31,19 @@ def sample_rows(m: int, n_random: int = 32, seed: int = 0) -> np.ndarray:
     return np.array(sorted(rows), dtype=np.int64)
 
 
+def scale_arg(scale):
+    """A device scale tensor as the oracle takes it: None, one float, or N per-column fp32 values."""
+    if scale is None:
+        return None
+    if scale.numel() == 1:
+        return float(scale.item())
+    return scale.detach().float().cpu().numpy()
+
+
 def oracle_ref(a: torch.Tensor, b_prepacked: torch.Tensor, scale, bias, out_dtype, rows=None) -> np.ndarray:
     """Oracle output bits for device inputs (all rows, or the given subset)."""
     return oracle.scaled_mm(
-        bits_of(a), FMT_OF[a.dtype], bits_of(b_prepacked), FMT_OF[b_prepacked.dtype],
-        None if scale is None else float(scale.item()),
+        bits_of(a), FMT_OF[a.dtype], bits_of(b_prepacked), FMT_OF[b_prepacked.dtype], scale_arg(scale),
         None if bias is None else bits_of(bias), FMT_OF[out_dtype], rows=rows, threads=16,
     )
 
@@ -64,7 +72,7 @@ def check_against_oracle(out: torch.Tensor, a, b_prepacked, scale, bias, rows=No
         return res
     lo, hi = oracle.scaled_mm_band(
         bits_of(a), FMT_OF[a.dtype], bits_of(b_prepacked), FMT_OF[b_prepacked.dtype],
-        None if scale is None else float(scale.item()), None if bias is None else bits_of(bias), fmt,
+        scale_arg(scale), None if bias is None else bits_of(bias), fmt,
         BAND_REL * res["rms"], rows=rows, threads=16)
     got_f = oracle.bits_to_f32(got, fmt).astype(np.float64)
     ref_f = oracle.bits_to_f32(ref, fmt).astype(np.float64)

@@ -65,6 +65,8 @@ def _call(lib, a=A, b=B, s=S, bias=BIAS, c=C, M=64, N=128, K=256, has_scale=1, h
     dict(c=C + 2),
     dict(bias=BIAS + 2),
     dict(has_scale=1, s=None),
+    dict(has_scale=2, s=S + 4),                # per-column scales must be 16-byte aligned
+    dict(has_scale=2, s=None),
     dict(a=None),
     dict(M=1 << 20, K=1 << 11),                # a would be 4 GiB
 ])

@@ -192,6 +192,57 @@ def test_power_of_two_scale_is_exact_and_linear():
     assert np.array_equal(y1 * 8, y8)
 
 
+def test_per_column_power_of_two_scales_scale_each_column():
+    """Distinct power-of-two scales per output column (`naive.py:29-33`, bias_dim = 1): column n is
+    exactly the unscaled column times scale[n]; a row/column mix-up would scale rows instead."""
+    rng = np.random.default_rng(14)
+    m, k, n = 7, 80, 24
+    a = _f16(rng.normal(size=(m, k)))
+    b = torch.tensor(rng.normal(size=(k, n)), dtype=torch.float32).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    p = oracle.prepack(b)
+    col = np.exp2(rng.integers(-6, 7, size=n)).astype(np.float32)
+    assert len(set(col.tolist())) > 4
+    y1 = oracle.scaled_mm_f32(a, oracle.F16, p, oracle.E5M2, None)
+    yc = oracle.scaled_mm_f32(a, oracle.F16, p, oracle.E5M2, col)
+    assert np.array_equal(y1 * col[None, :], yc)
+    assert not np.array_equal(yc, y1 * col[:m, None])  # the row-wise (bias_dim = 0) reading
+
+
+def test_constant_column_scales_equal_the_per_tensor_scale():
+    rng = np.random.default_rng(15)
+    a_bits, packed, scale, _ = oracle.make_inputs(9, 144, 40, oracle.BF16, seed=3)
+    bias = oracle.f32_to_bf16(rng.normal(size=40).astype(np.float32))
+    one = oracle.scaled_mm(a_bits, oracle.BF16, packed, oracle.E5M2, scale, bias, oracle.BF16)
+    vec = oracle.scaled_mm(a_bits, oracle.BF16, packed, oracle.E5M2, np.full(40, scale, np.float32), bias,
+                           oracle.BF16)
+    assert np.array_equal(one, vec)
+
+
+def test_per_column_scale_brute_force_tiny():
+    rng = np.random.default_rng(16)
+    m, k, n = 2, 32, 8
+    a = _f16(rng.normal(size=(m, k)))
+    codes = rng.integers(0, 0x7B, size=(k, n), dtype=np.uint8)
+    col = rng.uniform(0.01, 3.0, size=n).astype(np.float32)
+    bias = _f16(rng.normal(size=n))
+    out = oracle.scaled_mm(a, oracle.F16, oracle.prepack(codes), oracle.E5M2, col, bias, oracle.F16)
+    af = a.view(np.float16).astype(np.float64)
+    bf = (codes.astype(np.uint16) << 8).view(np.float16).astype(np.float64)
+    for i in range(m):
+        for j in range(n):
+            s = sum(af[i, kk] * bf[kk, j] for kk in range(k))
+            y = np.float16(np.float32(s) * col[j])
+            y = np.float16(np.float32(y) + np.float32(bias.view(np.float16)[j]))
+            assert out[i, j] == np.array([y]).view(np.uint16)[0]
+
+
+def test_scale_of_the_wrong_length_is_refused():
+    a = np.zeros((2, 16), np.uint16)
+    p = oracle.prepack(np.zeros((16, 8), np.uint8))
+    with pytest.raises(AssertionError):
+        oracle.scaled_mm(a, oracle.F16, p, oracle.E5M2, np.ones(7, np.float32), None, oracle.F16)
+
+
 def test_brute_force_float64_loops_tiny():
     rng = np.random.default_rng(5)
     m, k, n = 3, 32, 8
