@@ -15,6 +15,11 @@ Run from `feather-ops_amd/`:
     python -m benchmarks.benchmark_scaled_mm_hip --tiles                # every instantiated tile as well
     python -m benchmarks.benchmark_scaled_mm_hip --tiles "2,2,4,4,8,1;8,1,4,1,4,0"
     python -m benchmarks.benchmark_scaled_mm_hip --cells "4096,12288,3072" --cold
+    python -m benchmarks.benchmark_scaled_mm_hip --tiles --splits 2,3,4,6,8   # split-K candidates too
+
+`auto` is the whole heuristic (tile and split count). With `--splits`, every listed ring tile whose grid
+has fewer tiles than the GPU has compute units is also timed split `S` ways (named `(tile)/S`), for each
+`S` that keeps at most four workgroups per CU.
 """
 
 import argparse
@@ -29,8 +34,15 @@ sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
 
 from benchmarks.cells import GROUPS, cells  # noqa: E402
 from benchmarks.protocol import measure, paired_speedup  # noqa: E402
-from feather_ops.scaled_mm import prepack_b_for_scaled_mm, select_scaled_mm_config  # noqa: E402
-from feather_ops.tiles import SCALED_MM_TILES  # noqa: E402
+from feather_ops.scaled_mm import (  # noqa: E402
+    _launch,
+    prepack_b_for_scaled_mm,
+    select_scaled_mm_config,
+    select_scaled_mm_splits,
+)
+from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, split_workspace_bytes  # noqa: E402
+
+_CUS = 256
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}
 
@@ -75,19 +87,30 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     op = torch.ops.feather_ops.scaled_mm.default
 
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, out_dtype))
+    picked_splits = select_scaled_mm_splits(m, n, k, picked)
     providers = {"torch_mm": lambda i: torch.mm(control_a, control_w.t())}
-    if picked not in tiles:  # when the sweep includes the picked tile, `auto` is that tile's measurement
-        providers["auto"] = lambda i: op(a, packs[i % copies], scale, bias, out, *picked)
     for tile in tiles:
         providers[str(tile)] = lambda i, tile=tile: op(a, packs[i % copies], scale, bias, out, *tile)
+        if tile[5] != 1:
+            continue
+        bm, bn, _ = gemm_block_sizes(tile)
+        grid = -(-m // bm) * -(-n // bn)
+        for splits in args.splits:
+            if grid < _CUS and grid * splits <= 4 * _CUS and split_workspace_bytes(m, n, k, tile, splits) > 0:
+                providers[f"{tile}/{splits}"] = lambda i, tile=tile, splits=splits: _launch(
+                    a, packs[i % copies], scale, bias, out, tile, splits)
+    auto_name = str(picked) if picked_splits == 1 else f"{picked}/{picked_splits}"
+    if auto_name not in providers:  # when the sweep includes the pick, `auto` is that measurement
+        providers["auto"] = lambda i: _launch(a, packs[i % copies], scale, bias, out, picked, picked_splits)
     res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms)
-    if picked in tiles:
-        res["auto"] = res[str(picked)]
+    if "auto" not in res:
+        res["auto"] = res[auto_name]
     tflops = {name: 2.0 * m * n * k / (r.median_ms * 1e-3) / 1e12 for name, r in res.items()}
-    tile_names = [str(t) for t in tiles] or ["auto"]
+    tile_names = [name for name in providers if name not in ("torch_mm", "auto")] or ["auto"]
     best = max(tile_names, key=lambda name: tflops[name])
     return {
-        "M": m, "N": n, "K": k, "weight_copies": copies, "picked": list(picked), "best": best,
+        "M": m, "N": n, "K": k, "weight_copies": copies, "picked": list(picked), "picked_splits": picked_splits,
+        "best": best,
         "tflops": tflops, "median_ms": {name: r.median_ms for name, r in res.items()},
         "spread": {name: (r.p80_ms - r.p20_ms) / r.median_ms for name, r in res.items()},
         "auto_vs_torch_mm": paired_speedup(res["auto"], res["torch_mm"]),
@@ -101,6 +124,7 @@ def main() -> int:
     parser.add_argument("--groups", default="", help=f"comma-separated groups of cells.py: {','.join(GROUPS)}")
     parser.add_argument("--square", action="store_true", help="N^3 for N in 512..8192 instead of the grid")
     parser.add_argument("--tiles", nargs="?", const="", default=None, help="'m,n,u,rm,rn,p;...', or nothing for all")
+    parser.add_argument("--splits", default="", help="'2,3,4': split-K counts to time for underfilled ring grids")
     parser.add_argument("--a-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--out-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--no-bias", dest="bias", action="store_false")
@@ -115,6 +139,7 @@ def main() -> int:
         return 2
 
     tiles = parse_tiles(args.tiles) if args.tiles is not None else []
+    args.splits = [int(v) for v in args.splits.split(",") if v.strip()]
     if args.square:
         shapes = [("square", s, s, s) for s in (512, 1024, 2048, 4096, 8192)]
     elif args.cells:
@@ -130,7 +155,8 @@ def main() -> int:
         results.append(r)
         t = r["tflops"]
         print(f"{group + ' ' + f'{m}x{n}x{k}':34s} {t['torch_mm']:9.1f} {t['auto']:9.1f} {t[r['best']]:9.1f}"
-              f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])} -> {r['best']}",
+              f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])}"
+              f"{'/' + str(r['picked_splits']) if r['picked_splits'] > 1 else ''} -> {r['best']}",
               flush=True)
         torch.cuda.empty_cache()
     geo = lambda xs: math.exp(sum(math.log(x) for x in xs) / len(xs))  # noqa: E731

@@ -24,12 +24,21 @@ bool is_aligned(const void* p, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
 }
 
-// feather_ops::scaled_mm. Preconditions and messages follow csrc/hip_kernel.cu:729-801; N is relaxed from
-// a multiple of 16 to a multiple of 8 (16-byte output rows stay aligned, partial 16-column tiles are masked),
-// and scale may also hold one value per output column (the per-channel scale of feather_ops/naive.py:29-33).
-void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
-               const std::optional<Tensor>& bias, Tensor& c, const int64_t block_warps_m, const int64_t block_warps_n,
-               const int64_t unroll_k, const int64_t repeat_m, const int64_t repeat_n, const bool prefetch) {
+// What the C ABI needs of one validated scaled_mm call.
+struct Operands {
+    int64_t M, N, K;
+    int scale_mode;  // 0: none, 1: per tensor, 2: per output column
+    bool e5m2, a_bf16, out_bf16;
+    int32_t device_index;
+};
+
+// Preconditions and messages of feather_ops::scaled_mm, following csrc/hip_kernel.cu:729-801; N is relaxed
+// from a multiple of 16 to a multiple of 8 (16-byte output rows stay aligned, partial 16-column tiles are
+// masked), and scale may also hold one value per output column (the per-channel scale of
+// feather_ops/naive.py:29-33).
+Operands check_operands(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
+                        const std::optional<Tensor>& bias, const Tensor& c, const int64_t block_warps_m,
+                        const int64_t block_warps_n) {
     STD_TORCH_CHECK(a.is_cuda(), "a must be a CUDA tensor");
     STD_TORCH_CHECK(b_prepacked.is_cuda(), "b_prepacked must be a CUDA tensor");
     STD_TORCH_CHECK(c.is_cuda(), "c must be a CUDA tensor");
@@ -98,27 +107,78 @@ void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<T
     STD_TORCH_CHECK(M * K * 2 < (int64_t{1} << 31) && M * N * 2 < (int64_t{1} << 31) &&
                         b_prepacked.size(0) * N * 16 < (int64_t{1} << 31),
                     "a, b_prepacked and c must each be smaller than 2 GiB");
-    if (M == 0) return;
+    if (M > 0) {
+        STD_TORCH_CHECK(is_aligned(a.const_data_ptr(), 16), "a data pointer must be 16-byte aligned");
+        STD_TORCH_CHECK(is_aligned(b_prepacked.const_data_ptr(), 16),
+                        "b_prepacked data pointer must be 16-byte aligned");
+        STD_TORCH_CHECK(is_aligned(c.const_data_ptr(), 16), "c data pointer must be 16-byte aligned");
+    }
+    return Operands{M, N, K, scale_mode, b_type == ST::Float8_e5m2, a_type == ST::BFloat16,
+                    c.scalar_type() == ST::BFloat16, device_index};
+}
 
-    torch::stable::accelerator::DeviceGuard guard(device_index);
+hipStream_t current_stream(int32_t device_index) {
     void* raw_stream = nullptr;
     TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &raw_stream));
+    return static_cast<hipStream_t>(raw_stream);
+}
 
-    STD_TORCH_CHECK(is_aligned(a.const_data_ptr(), 16), "a data pointer must be 16-byte aligned");
-    STD_TORCH_CHECK(is_aligned(b_prepacked.const_data_ptr(), 16), "b_prepacked data pointer must be 16-byte aligned");
-    STD_TORCH_CHECK(is_aligned(c.mutable_data_ptr(), 16), "c data pointer must be 16-byte aligned");
+void check_launch(bool launched, const char* what) {
+    STD_TORCH_CHECK(launched, "Unsupported config");
+    const hipError_t err = hipGetLastError();
+    STD_TORCH_CHECK(err == hipSuccess, what, " kernel launch failed: ", hipGetErrorString(err));
+}
 
+// feather_ops::scaled_mm (csrc/hip_kernel.cu:716-823 of the reference).
+void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
+               const std::optional<Tensor>& bias, Tensor& c, const int64_t block_warps_m, const int64_t block_warps_n,
+               const int64_t unroll_k, const int64_t repeat_m, const int64_t repeat_n, const bool prefetch) {
+    const Operands o = check_operands(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n);
+    if (o.M == 0) return;
+    torch::stable::accelerator::DeviceGuard guard(o.device_index);
     const bool launched = launch_scaled_mm(
         static_cast<const uint16_t*>(a.const_data_ptr()), static_cast<const uint8_t*>(b_prepacked.const_data_ptr()),
         scale.has_value() ? static_cast<const float*>(scale->const_data_ptr()) : nullptr,
         bias.has_value() ? static_cast<const uint16_t*>(bias->const_data_ptr()) : nullptr,
-        static_cast<uint16_t*>(c.mutable_data_ptr()), M, N, K, scale_mode, bias.has_value() ? 1 : 0,
-        b_type == ST::Float8_e5m2, a_type == ST::BFloat16, c.scalar_type() == ST::BFloat16,
-        static_cast<int>(block_warps_m), static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
-        static_cast<int>(repeat_m), static_cast<int>(repeat_n), prefetch, static_cast<hipStream_t>(raw_stream));
-    STD_TORCH_CHECK(launched, "Unsupported config");
-    const hipError_t err = hipGetLastError();
-    STD_TORCH_CHECK(err == hipSuccess, "scaled_mm kernel launch failed: ", hipGetErrorString(err));
+        static_cast<uint16_t*>(c.mutable_data_ptr()), o.M, o.N, o.K, o.scale_mode, bias.has_value() ? 1 : 0, o.e5m2,
+        o.a_bf16, o.out_bf16, static_cast<int>(block_warps_m), static_cast<int>(block_warps_n),
+        static_cast<int>(unroll_k), static_cast<int>(repeat_m), static_cast<int>(repeat_n), prefetch,
+        current_stream(o.device_index));
+    check_launch(launched, "scaled_mm");
+}
+
+// feather_ops::scaled_mm_splitk: scaled_mm on a ring-kernel tile with each tile's K range split over
+// `splits` workgroups that meet in `workspace` (uint8, the caller's; all zero before its first use, and
+// every completed call leaves it reusable; see feather_scaled_mm_splitk). No counterpart in the reference.
+void scaled_mm_splitk(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
+                      const std::optional<Tensor>& bias, Tensor& c, Tensor& workspace, const int64_t splits,
+                      const int64_t block_warps_m, const int64_t block_warps_n, const int64_t unroll_k,
+                      const int64_t repeat_m, const int64_t repeat_n) {
+    const Operands o = check_operands(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n);
+    STD_TORCH_CHECK(workspace.is_cuda() && workspace.get_device_index() == o.device_index,
+                    "workspace must be on the same device as a");
+    STD_TORCH_CHECK(workspace.scalar_type() == ST::Byte && workspace.dim() == 1 && workspace.stride(0) == 1,
+                    "workspace must be a contiguous 1-D uint8 tensor");
+    STD_TORCH_CHECK(splits >= 1 && splits <= 32, "splits must be in 1 .. 32");
+    if (o.M == 0) return;
+    const int64_t need = feather_splitk_workspace_bytes(o.M, o.N, o.K, static_cast<int>(block_warps_m),
+                                                        static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
+                                                        static_cast<int>(repeat_m), static_cast<int>(repeat_n),
+                                                        static_cast<int>(splits));
+    STD_TORCH_CHECK(need >= 0, "Unsupported config");
+    STD_TORCH_CHECK(splits == 1 || workspace.numel() >= need, "workspace must hold at least ", need, " bytes");
+    STD_TORCH_CHECK(splits == 1 || is_aligned(workspace.const_data_ptr(), 256),
+                    "workspace data pointer must be 256-byte aligned");
+    torch::stable::accelerator::DeviceGuard guard(o.device_index);
+    const bool launched = feather_scaled_mm_splitk(
+        static_cast<const uint16_t*>(a.const_data_ptr()), static_cast<const uint8_t*>(b_prepacked.const_data_ptr()),
+        scale.has_value() ? static_cast<const float*>(scale->const_data_ptr()) : nullptr,
+        bias.has_value() ? static_cast<const uint16_t*>(bias->const_data_ptr()) : nullptr,
+        static_cast<uint16_t*>(c.mutable_data_ptr()), o.M, o.N, o.K, o.scale_mode, bias.has_value() ? 1 : 0, o.e5m2,
+        o.a_bf16, o.out_bf16, static_cast<int>(block_warps_m), static_cast<int>(block_warps_n),
+        static_cast<int>(unroll_k), static_cast<int>(repeat_m), static_cast<int>(repeat_n), static_cast<int>(splits),
+        workspace.mutable_data_ptr(), workspace.numel(), current_stream(o.device_index));
+    check_launch(launched, "scaled_mm_splitk");
 }
 
 // feather_ops::bf16_to_fp16: out = bf16 -> fp16 (round toward zero) of x, both contiguous on one device.
@@ -182,12 +242,17 @@ STABLE_TORCH_LIBRARY(feather_ops, m) {
     m.def(
         "scaled_mm(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, int block_warps_m, "
         "int block_warps_n, int unroll_k, int repeat_m, int repeat_n, bool prefetch) -> ()");
+    m.def(
+        "scaled_mm_splitk(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, "
+        "Tensor(b!) workspace, int splits, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, "
+        "int repeat_n) -> ()");
     m.def("bf16_to_fp16(Tensor x, Tensor(a!) out) -> ()");
     m.def("prepack_b(Tensor b, Tensor(a!) out) -> ()");
 }
 
 STABLE_TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm", TORCH_BOX(&scaled_mm));
+    m.impl("scaled_mm_splitk", TORCH_BOX(&scaled_mm_splitk));
     m.impl("bf16_to_fp16", TORCH_BOX(&bf16_to_fp16));
     m.impl("prepack_b", TORCH_BOX(&prepack_b));
 }

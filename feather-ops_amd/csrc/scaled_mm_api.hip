@@ -1,6 +1,7 @@
 // C ABI of the gfx950 scaled matmul (include/feather_ops.h). Validates the contract on the host, so an
 // out-of-contract call enqueues nothing, then routes to the instantiation of its dtype combination.
 #include "feather_ops.h"
+#include "feather_tiles.h"
 #include "scaled_mm_launch.h"
 
 #include <cstdint>
@@ -9,6 +10,10 @@ namespace feather {
 namespace {
 
 constexpr int64_t kMaxBufferBytes = (int64_t{1} << 31) - 1;  // buffer offsets are 31-bit (kOob marks "out")
+constexpr int kMaxSplits = 32;
+// The arrival counters occupy a fixed area at the start of every split workspace, whatever the shape, so
+// a workspace reused across shapes never has partial sums where a later call keeps its counters.
+constexpr int64_t kSplitCtrBytes = 64 * 1024;
 
 bool aligned(const void* ptr, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0;
@@ -31,29 +36,45 @@ bool contract_ok(const uint16_t* a, const uint8_t* b, const float* scale, const 
     return true;
 }
 
-}  // namespace
-}  // namespace feather
+// True for a ring-kernel (prefetch = 1) tile of the instantiated table: the only kernel that splits K.
+bool is_ring_tile(int wm, int wn, int u, int rm, int rn) {
+#define FEATHER_IS_RING_TILE(twm, twn, tu, trm, trn, tpf) \
+    || ((tpf) != 0 && wm == (twm) && wn == (twn) && u == (tu) && rm == (trm) && rn == (trn))
+    return false FEATHER_SCALED_MM_TILES(FEATHER_IS_RING_TILE);
+#undef FEATHER_IS_RING_TILE
+}
 
-extern "C" bool launch_scaled_mm(const uint16_t* const a, const uint8_t* const b_prepacked, const float* const scale,
-                                 const uint16_t* const bias, uint16_t* const c, const int64_t M, const int64_t N,
-                                 const int64_t K, const int has_scale, const int has_bias, const bool use_fp8_e5m2,
-                                 const bool a_bf16, const bool output_bf16, const int block_warps_m,
-                                 const int block_warps_n, const int unroll_k, const int repeat_m, const int repeat_n,
-                                 const bool prefetch, hipStream_t stream) {
-    using namespace feather;
-    if (!contract_ok(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias)) return false;
-    Params p{};
-    p.a = a;
-    p.b = b_prepacked;
-    p.scale = has_scale ? scale : nullptr;
-    p.col_scale = has_scale == 2 ? 1 : 0;
-    p.bias = has_bias ? bias : nullptr;
-    p.c = c;
-    p.M = static_cast<int32_t>(M);
-    p.N = static_cast<int32_t>(N);
-    p.K = static_cast<int32_t>(K);
-    p.kb_total = static_cast<int32_t>((K + 127) / 128 * 8);
-    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
+// Workspace of a split launch: the counter area (one uint32 per tile and wave, at most kSplitCtrBytes), then
+// the partial sums (splits fp32 tiles per output tile); none for splits = 1. -1 when the tile, the split
+// count or the grid is out of contract.
+struct SplitLayout {
+    int64_t ctr_bytes = -1;
+    int64_t total_bytes = -1;
+};
+
+SplitLayout split_layout(int64_t M, int64_t N, int64_t K, int wm, int wn, int u, int rm, int rn, int splits) {
+    SplitLayout l;
+    if (M < 1 || N < 1 || K < 16 || !is_ring_tile(wm, wn, u, rm, rn)) return l;
+    const int64_t stages = (K + 16 * u - 1) / (16 * u);
+    if (splits < 1 || splits > kMaxSplits || splits > stages) return l;
+    if (splits == 1) {  // the unsplit kernel: no workspace
+        l.ctr_bytes = 0;
+        l.total_bytes = 0;
+        return l;
+    }
+    const int64_t bm = 16 * wm * rm;
+    const int64_t bn = 16 * wn * rn;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    if (tiles * wm * wn * 4 > kSplitCtrBytes) return l;
+    const int64_t total = kSplitCtrBytes + tiles * splits * bm * bn * 4;
+    if (total > kMaxBufferBytes) return l;
+    l.ctr_bytes = kSplitCtrBytes;
+    l.total_bytes = total;
+    return l;
+}
+
+bool launch(const Params& p, bool use_fp8_e5m2, bool a_bf16, bool output_bf16, const TileQuery& t,
+            hipStream_t stream) {
     const int combo = (use_fp8_e5m2 ? 4 : 0) | (a_bf16 ? 2 : 0) | (output_bf16 ? 1 : 0);
     switch (combo) {
         case 0: return launch_combo_000(t, p, stream);
@@ -65,4 +86,68 @@ extern "C" bool launch_scaled_mm(const uint16_t* const a, const uint8_t* const b
         case 6: return launch_combo_110(t, p, stream);
         default: return launch_combo_111(t, p, stream);
     }
+}
+
+Params make_params(const uint16_t* a, const uint8_t* b_prepacked, const float* scale, const uint16_t* bias,
+                   uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale, int has_bias) {
+    Params p{};
+    p.a = a;
+    p.b = b_prepacked;
+    p.scale = has_scale ? scale : nullptr;
+    p.bias = has_bias ? bias : nullptr;
+    p.c = c;
+    p.M = static_cast<int32_t>(M);
+    p.N = static_cast<int32_t>(N);
+    p.K = static_cast<int32_t>(K);
+    p.kb_total = static_cast<int32_t>((K + 127) / 128 * 8);
+    p.col_scale = has_scale == 2 ? 1 : 0;
+    p.splits = 1;
+    return p;
+}
+
+}  // namespace
+}  // namespace feather
+
+extern "C" bool launch_scaled_mm(const uint16_t* const a, const uint8_t* const b_prepacked, const float* const scale,
+                                 const uint16_t* const bias, uint16_t* const c, const int64_t M, const int64_t N,
+                                 const int64_t K, const int has_scale, const int has_bias, const bool use_fp8_e5m2,
+                                 const bool a_bf16, const bool output_bf16, const int block_warps_m,
+                                 const int block_warps_n, const int unroll_k, const int repeat_m, const int repeat_n,
+                                 const bool prefetch, hipStream_t stream) {
+    using namespace feather;
+    if (!contract_ok(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias)) return false;
+    const Params p = make_params(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias);
+    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
+    return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);
+}
+
+extern "C" int64_t feather_splitk_workspace_bytes(const int64_t M, const int64_t N, const int64_t K,
+                                                  const int block_warps_m, const int block_warps_n,
+                                                  const int unroll_k, const int repeat_m, const int repeat_n,
+                                                  const int splits) {
+    return feather::split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, splits)
+        .total_bytes;
+}
+
+extern "C" bool feather_scaled_mm_splitk(const uint16_t* const a, const uint8_t* const b_prepacked,
+                                         const float* const scale, const uint16_t* const bias, uint16_t* const c,
+                                         const int64_t M, const int64_t N, const int64_t K, const int has_scale,
+                                         const int has_bias, const bool use_fp8_e5m2, const bool a_bf16,
+                                         const bool output_bf16, const int block_warps_m, const int block_warps_n,
+                                         const int unroll_k, const int repeat_m, const int repeat_n, const int splits,
+                                         void* const workspace, const int64_t workspace_bytes, hipStream_t stream) {
+    using namespace feather;
+    if (!contract_ok(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias)) return false;
+    const SplitLayout l =
+        split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, splits);
+    if (l.total_bytes < 0) return false;
+    if (splits > 1 && (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total_bytes)) return false;
+    Params p = make_params(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias);
+    if (splits > 1) {
+        p.splits = splits;
+        p.split_ctr = static_cast<uint32_t*>(workspace);
+        p.split_part = static_cast<uint8_t*>(workspace) + l.ctr_bytes;
+    }
+    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, true};
+    return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);
 }

@@ -60,6 +60,11 @@ struct Params {
     int32_t M, N, K;
     int32_t kb_total;           // b_prepacked.shape[0]
     int32_t col_scale;          // scale holds one value per output column (16-byte aligned)
+    // Split-K (ring kernel only): each output tile's 64-deep stages are cut into `splits` contiguous
+    // ranges, one workgroup per range. 1 = no split; then the two pointers are unused.
+    int32_t splits;
+    uint32_t* split_ctr;        // [tiles * waves] arrival counters: zero before a launch, zero after it
+    uint8_t* split_part;        // [tiles][splits][waves][RM * RN][64 lanes] fp32x4 partial sums
 };
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -299,6 +304,60 @@ __device__ __forceinline__ void tile_of_block(int bid, int nblocks, int tiles_m,
     tn = in / gm;
 }
 
+// ---- split-K join ------------------------------------------------------------------------------------------
+
+// Buffer instruction cache-policy bit that makes a load or store coherent at device (agent) scope on gfx950:
+// stores write through to the point shared by all XCDs, loads never return a stale cached line. (It is the
+// bit the compiler itself sets for relaxed agent-scope atomic loads and stores.)
+constexpr int kDeviceScope = 16;
+
+// One wave's side of the split-K join, after its K range is accumulated. The wave parks its partial sums in
+// its slot of the workspace with device-coherent stores, waits until they are written, and counts itself in
+// at its (tile, wave) counter. The last of the tile's `splits` waves to arrive reads every partial back,
+// adds them in split order 0, 1, ..., splits - 1 (the same order whichever arrives last, so results are
+// deterministic), resets the counter to zero for the next launch and returns true: it then stores the tile.
+// The others return false and end. No wave ever waits for another workgroup, so the join cannot stall
+// whatever the dispatch order. Agent-scope fences would do instead of the coherent accesses, but they write
+// back and invalidate the whole L2 of the XCD under every co-resident workgroup (measured 1.5-2x slower).
+template <int kWaves, int RM, int RN>
+__device__ __forceinline__ bool join_split(const Params& p, f32x4 (&acc)[RM][RN], int tile_id, int split, int wave,
+                                           int lane) {
+    constexpr uint32_t kSlotBytes = RM * RN * kWave * 16;
+    const rsrc_t part = make_rsrc(p.split_part, 0x7fffffffu);
+    const auto slot = [&](int s) {
+        return (static_cast<uint32_t>(tile_id * p.splits + s) * kWaves + static_cast<uint32_t>(wave)) * kSlotBytes +
+               static_cast<uint32_t>(lane) * 16u;
+    };
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), part,
+                                                   slot(split) + (i * RN + j) * kWave * 16u, 0, kDeviceScope);
+    // The stores must be complete (visible at device scope) before the counter says so; the memory clobber
+    // keeps the compiler from moving the atomic above them.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint32_t* ctr = p.split_ctr + tile_id * kWaves + wave;
+    uint32_t arrived = 0;
+    if (lane == 0) arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    asm volatile("" ::: "memory");  // the partial reads below stay after the atomic
+    if (arrived != static_cast<uint32_t>(p.splits - 1)) return false;
+    for (int s = 0; s < p.splits; ++s) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int j = 0; j < RN; ++j) {
+                const f32x4 v = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, slot(s) + (i * RN + j) * kWave * 16u, 0,
+                                                                 kDeviceScope));
+                acc[i][j] = s == 0 ? v : acc[i][j] + v;
+            }
+    }
+    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // ---- ring kernel: direct-to-LDS loads, LDS ring of 64-deep stages -----------------------------------------
 
 // s_waitcnt immediate that waits until at most n vector-memory operations of this wave are outstanding
@@ -409,7 +468,9 @@ __device__ __forceinline__ int a_unit_phys(int row, int u) {
     return u ^ a_swizzle_key<kUnits>(row);
 }
 
-template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16>
+// kSplitK: this launch splits K (p.splits > 1). A separate instantiation, so the unsplit kernel carries no
+// join code (its partial reads raise register pressure: measured 3% slower on a 128 x 256 tile).
+template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK>
 __global__ __launch_bounds__(kWave * WM * WN)
 __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) void ring_dma_kernel(const Params p) {
     using S = DmaShape<WM, WN, U, RM, RN>;
@@ -423,15 +484,25 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
 
     const int tiles_m = (p.M + S::kBM - 1) / S::kBM;
     const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
+    // Workgroup -> (K range, tile): split-major, so the workgroups of one K range walk the tiles in the
+    // XCD-aware order and share operand panels as the unsplit grid does.
+    const int n_tiles = tiles_m * tiles_n;
+    const int splits = kSplitK ? p.splits : 1;
+    const int split = kSplitK ? static_cast<int>(blockIdx.x) / n_tiles : 0;
+    const int tile_id = static_cast<int>(blockIdx.x) - split * n_tiles;
     int tm, tn;
-    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    tile_of_block(tile_id, n_tiles, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * S::kBM;
     const int n0 = tn * S::kBN;
 
     const rsrc_t a_rsrc = make_rsrc(p.a, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.K) * 2u);
     const rsrc_t b_rsrc = make_rsrc(p.b, static_cast<uint32_t>(p.kb_total) * static_cast<uint32_t>(p.N) * 16u);
     const int k_chunks = p.K / 16;
-    const int stages = (p.K + 16 * U - 1) / (16 * U);
+    // This workgroup's stages: global stages [stage0, stage0 + stages). Loads address global stages; the
+    // ring slots and the wait schedule count local ones.
+    const int stages_total = (p.K + 16 * U - 1) / (16 * U);
+    const int stage0 = split * stages_total / splits;
+    const int stages = (split + 1) * stages_total / splits - stage0;
     const float scale = load_scale(p);
     const int full_stages = k_chunks / U;  // stages with every chunk inside K
 
@@ -473,7 +544,8 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
     // shortens their activation lead from two stages to one and measured 11% slower).
     constexpr bool kStageA = kABf16 && S::kWaves <= 4;
     u32x4 a_regs[S::kAInstr];
-    auto load_a = [&](int stage) {
+    auto load_a = [&](int local_stage) {
+        const int stage = stage0 + local_stage;
         const uint32_t soff = static_cast<uint32_t>(stage) * static_cast<uint32_t>(U) * 32u;
         if (stage < full_stages) {
 #pragma unroll
@@ -493,8 +565,9 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
             *reinterpret_cast<u32x4*>(base + (wave + i * S::kWaves) * 1024) = bf16x8_to_f16x8(a_regs[i]);
         }
     };
-    auto issue_a = [&](int stage) {
-        uint8_t* base = lds + (stage % S::kSlotsA) * S::kABytes;
+    auto issue_a = [&](int local_stage) {
+        uint8_t* base = lds + (local_stage % S::kSlotsA) * S::kABytes;
+        const int stage = stage0 + local_stage;
         const uint32_t soff = static_cast<uint32_t>(stage) * static_cast<uint32_t>(U) * 32u;
         if (stage < full_stages) {
 #pragma unroll
@@ -507,8 +580,9 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
             }
         }
     };
-    auto issue_b = [&](int stage) {
-        uint8_t* base = lds + S::kBRing + (stage % S::kSlotsB) * S::kBBytes;
+    auto issue_b = [&](int local_stage) {
+        uint8_t* base = lds + S::kBRing + (local_stage % S::kSlotsB) * S::kBBytes;
+        const int stage = stage0 + local_stage;
         const uint32_t soff = static_cast<uint32_t>(stage) * b_stage_stride;
         if (stage < full_stages) {
 #pragma unroll
@@ -630,6 +704,9 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
         }
     }
 
+    if constexpr (kSplitK) {
+        if (!join_split<S::kWaves, RM, RN>(p, acc, tile_id, split, wave, lane)) return;
+    }
     store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale);
 }
 

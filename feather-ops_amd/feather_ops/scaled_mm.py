@@ -20,12 +20,13 @@ import torch
 from torch.library import custom_op
 
 from . import _lib
-from .tiles import gemm_block_sizes
+from .tiles import gemm_block_sizes, split_workspace_bytes
 
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
 _TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
 _TILE_RING_256x256 = (4, 2, 4, 4, 8, 1)
 _TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
+_TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
 _TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
 _TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
 
@@ -38,7 +39,12 @@ _RING_MODEL = (
     (_TILE_RING_128x256, 2, 1100.0),
     (_TILE_RING_256x256, 1, 1040.0),
     (_TILE_RING_128x128, 3, 1030.0),
+    (_TILE_RING_64x128, 3, 600.0),
 )
+
+# Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
+_SPLIT_MIN_K = 4096
+_SPLIT_MIN_STAGES = 16
 
 
 def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
@@ -63,19 +69,26 @@ def select_scaled_mm_config(
 ) -> tuple[int, int, int, int, int, int]:
     """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
 
-    Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile; the pick is within
-    1% of the best tile in geometric mean and within 8% everywhere):
+    Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile and split count;
+    with `select_scaled_mm_splits` the pick is within 1.2% of the best candidate in geometric mean):
     - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
-      blocks finish first (a wave-quantization model over 128 x 256, 256 x 256 and 128 x 128 tiles with
-      their measured full-grid rates).
-    - M > 64 with a smaller grid: the 64 x 64 ring tile once it gives 512 blocks, otherwise streaming.
+      blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
+      tiles with their measured full-grid rates).
+    - M > 64 with a smaller grid and K >= 4096: the 128 x 128 ring tile (96 tiles or more) or the
+      64 x 128 ring tile (48 or more 128 x 128 tiles), split along K (`select_scaled_mm_splits`).
+    - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
     - 16 < M <= 64: the 32-row streaming tile when it gives a CU's worth of blocks.
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
       columns), with 8 K slices per block unless there are 512 blocks or more, then 4.
     """
-    del K, a_dtype, b_dtype, out_dtype
-    if M > 64 and _blocks(M, N, _TILE_RING_128x128) >= _CUS:
+    del a_dtype, b_dtype, out_dtype
+    tiles_128 = _blocks(M, N, _TILE_RING_128x128)
+    if M > 64 and tiles_128 >= _CUS:
         return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
+    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 96:
+        return _TILE_RING_128x128
+    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 48:
+        return _TILE_RING_64x128
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
     if 16 < M <= 64 and _blocks(M, N, _TILE_STREAM_32x64) >= _CUS:
@@ -88,6 +101,47 @@ def select_scaled_mm_config(
     return (8 if blocks < 2 * _CUS else 4, 1, 4, 1, repeat_n, 0)
 
 
+def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> int:
+    """K splits for a tile `select_scaled_mm_config` picked (1: none). Not in the reference, whose kernel
+    has no split-K.
+
+    The split regime of `select_scaled_mm_config` (M > 64, K >= 4096, fewer 128 x 128 tiles than CUs)
+    splits its 128 x 128 or 64 x 128 ring tile into enough K ranges for about 512 workgroups (two per CU),
+    2 to 8 of them, each at least 16 stages of 64 deep. Measured 5-40% faster than the best unsplit tile
+    on the grid's cells in that regime; shorter K loses (the per-split fixed costs dominate).
+    """
+    tile = tuple(tile)
+    if M <= 64 or K < _SPLIT_MIN_K or tile not in (_TILE_RING_128x128, _TILE_RING_64x128):
+        return 1
+    if tile != select_scaled_mm_config(M, N, K):
+        return 1
+    tiles_128 = _blocks(M, N, _TILE_RING_128x128)
+    if tiles_128 >= _CUS:
+        return 1
+    stages = -(-K // 64)
+    return max(2, min(8, (2 * _CUS) // _blocks(M, N, tile), stages // _SPLIT_MIN_STAGES))
+
+
+# Split-K workspaces, one per (device, stream): the counter area at their start must be zero before a
+# launch, and every completed launch leaves it zero whatever its shape, so a workspace is zeroed once, when
+# it is created, and then reused by the launches of its stream, which are ordered. Other streams get their
+# own.
+_split_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _split_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    stream = torch.cuda.current_stream(device)
+    if torch.cuda.is_current_stream_capturing():
+        # Under graph capture the zero fill is recorded with the launch, so every replay starts clean.
+        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    ws = _split_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _split_workspaces[key] = ws
+    return ws
+
+
 def _launch(
     a: torch.Tensor,
     b_prepacked: torch.Tensor,
@@ -95,8 +149,16 @@ def _launch(
     bias: torch.Tensor | None,
     out: torch.Tensor,
     tile: tuple[int, int, int, int, int, int],
+    splits: int = 1,
 ) -> None:
-    torch.ops.feather_ops.scaled_mm.default(a, b_prepacked, scale, bias, out, *tile)
+    if splits == 1:
+        torch.ops.feather_ops.scaled_mm.default(a, b_prepacked, scale, bias, out, *tile)
+        return
+    nbytes = split_workspace_bytes(a.shape[0], b_prepacked.shape[1], a.shape[1], tile, splits)
+    if nbytes < 0:
+        raise RuntimeError(f"split-K needs a ring tile and 1 <= splits <= the K stage count, got {tile}, {splits}")
+    ws = _split_workspace(a.device, nbytes)
+    torch.ops.feather_ops.scaled_mm_splitk.default(a, b_prepacked, scale, bias, out, ws, splits, *tile[:5])
 
 
 @custom_op("feather_ops::scaled_mm_auto", mutates_args=("out",))
@@ -108,8 +170,9 @@ def _scaled_mm_auto(
     out: torch.Tensor,
 ) -> None:
     """The heuristic behind an opaque boundary: `torch.compile` does not specialize on its branches."""
-    tile = select_scaled_mm_config(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype, b_prepacked.dtype, out.dtype)
-    _launch(a, b_prepacked, scale, bias, out, tile)
+    M, N, K = a.shape[0], b_prepacked.shape[1], a.shape[1]
+    tile = select_scaled_mm_config(M, N, K, a.dtype, b_prepacked.dtype, out.dtype)
+    _launch(a, b_prepacked, scale, bias, out, tile, select_scaled_mm_splits(M, N, K, tile))
 
 
 def scaled_mm_hip(
@@ -119,17 +182,23 @@ def scaled_mm_hip(
     bias: torch.Tensor | None,
     out_dtype: torch.dtype,
     tile: tuple[int, int, int, int, int, int] | None = None,
+    splits: int | None = None,
 ) -> torch.Tensor:
     """`(a @ b^T) * scale + bias` against the prepacked fp8 weight `b_prepacked`.
 
-    `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it.
+    `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it. `splits` (not in the
+    reference) pins the split-K count of a ring tile; by default the heuristic picks it when `tile` is
+    None and a pinned tile runs unsplit.
     """
     _lib.require_native()
     out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
-    if tile is None:
+    if tile is None and splits is None:
         _scaled_mm_auto(a, b_prepacked, scale, bias, out)
     else:
-        _launch(a, b_prepacked, scale, bias, out, tile)
+        if tile is None:
+            tile = select_scaled_mm_config(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype,
+                                           b_prepacked.dtype, out_dtype)
+        _launch(a, b_prepacked, scale, bias, out, tile, 1 if splits is None else splits)
     return out
 
 

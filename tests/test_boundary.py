@@ -18,7 +18,7 @@ HEADER = ROOT / "include" / "feather_ops.h"
 
 def _declared():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return re.findall(r"^\s*bool\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:bool|int64_t)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 @pytest.fixture(scope="module")
@@ -34,12 +34,19 @@ def lib():
     handle.feather_prepack_b.restype = ctypes.c_bool
     handle.feather_prepack_b.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_void_p]
+    handle.feather_scaled_mm_splitk.restype = ctypes.c_bool
+    handle.feather_scaled_mm_splitk.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + \
+        [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 6 + [ctypes.c_void_p, ctypes.c_int64,
+                                                                           ctypes.c_void_p]
+    handle.feather_splitk_workspace_bytes.restype = ctypes.c_int64
+    handle.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 6
     return handle
 
 
 def test_library_exports_every_declared_symbol(lib):
     names = _declared()
-    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_prepack_b"}
+    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_prepack_b",
+                          "feather_scaled_mm_splitk", "feather_splitk_workspace_bytes"}
     for name in names:
         assert hasattr(lib, name), name
 
@@ -72,6 +79,46 @@ def _call(lib, a=A, b=B, s=S, bias=BIAS, c=C, M=64, N=128, K=256, has_scale=1, h
 ])
 def test_c_abi_refuses_out_of_contract_calls(lib, kwargs):
     assert _call(lib, **kwargs) is False
+
+
+WS = 0x100000  # fake, 256-byte aligned workspace address
+
+
+def _split(lib, tile=(2, 2, 4, 4, 4), splits=2, ws=WS, ws_bytes=1 << 30, M=64, N=128, K=256, c=C):
+    return lib.feather_scaled_mm_splitk(A, B, S, BIAS, c, M, N, K, 1, 1, True, False, False, *tile, splits, ws,
+                                        ws_bytes, None)
+
+
+@pytest.mark.parametrize("kwargs", [
+    dict(tile=(4, 1, 4, 1, 4)),            # a streaming tile: only the ring kernel splits K
+    dict(tile=(3, 3, 3, 3, 3)),            # not instantiated
+    dict(splits=0),
+    dict(splits=5),                        # K = 256 has 4 stages of 64
+    dict(splits=33, K=4096),               # above the 32 maximum
+    dict(ws=None),
+    dict(ws=WS + 16),                      # workspace not 256-byte aligned
+    dict(ws_bytes=1000),                   # workspace too small
+    dict(c=C + 2),                         # the launch_scaled_mm contract still applies
+])
+def test_splitk_c_abi_refuses_out_of_contract_calls(lib, kwargs):
+    assert _split(lib, **kwargs) is False
+
+
+def test_splitk_workspace_bytes_match_the_python_formula(lib):
+    from feather_ops.tiles import SCALED_MM_TILES, split_workspace_bytes
+
+    for tile in SCALED_MM_TILES:
+        for m, n, k in [(1, 8, 16), (67, 272, 304), (512, 5376, 5120), (4096, 3072, 3072)]:
+            for splits in (0, 1, 2, 3, 8, 32, 33):
+                want = lib.feather_splitk_workspace_bytes(m, n, k, *tile[:5], splits) if tile[5] else -1
+                assert split_workspace_bytes(m, n, k, tile, splits) == want, (tile, m, n, k, splits)
+    # 512 x 5376 with 128 x 128 tiles: the 64 KiB counter area, then 168 tiles x 3 fp32 partial tiles
+    assert lib.feather_splitk_workspace_bytes(512, 5376, 5120, 2, 2, 4, 4, 4, 3) == 65536 + 168 * 3 * 128 * 128 * 4
+    # 16384 (tile, wave) counters at most: 4096 128 x 128 tiles of 4 waves fit, 4097 do not
+    assert lib.feather_splitk_workspace_bytes(4096, 16384, 256, 2, 2, 4, 4, 4, 2) > 0
+    assert lib.feather_splitk_workspace_bytes(4096, 16392, 256, 2, 2, 4, 4, 4, 2) == -1
+    assert lib.feather_splitk_workspace_bytes(4096, 16392, 256, 2, 2, 4, 4, 4, 1) == 0  # unsplit: no workspace
+    assert lib.feather_splitk_workspace_bytes(512, 5376, 5120, 4, 1, 4, 1, 4, 2) == -1  # streaming tile
 
 
 def test_convert_c_abi_refuses_bad_arguments(lib):
@@ -121,6 +168,9 @@ def test_torch_ops_are_registered_for_the_gpu_only():
     with pytest.raises((NotImplementedError, RuntimeError)):
         torch.ops.feather_ops.prepack_b.default(torch.zeros(16, 8, dtype=torch.float8_e5m2),
                                                 torch.empty(8, 8, 16, dtype=torch.float8_e5m2))
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.feather_ops.scaled_mm_splitk.default(a, b, None, None, c, torch.zeros(1 << 16, dtype=torch.uint8),
+                                                       2, 2, 2, 4, 4, 4)
 
 
 def test_scaled_mm_hip_has_no_cpu_fallback():
@@ -130,6 +180,34 @@ def test_scaled_mm_hip_has_no_cpu_fallback():
     b = torch.zeros(8, 32, 16, dtype=torch.float8_e5m2)
     with pytest.raises((NotImplementedError, RuntimeError)):
         scaled_mm_hip(a, b, None, None, torch.float16)
+
+
+def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
+    """The split regime (fitted on the tile sweep): fewer 128 x 128 tiles than CUs and K >= 4096."""
+    from feather_ops.scaled_mm import select_scaled_mm_config as pick
+    from feather_ops.scaled_mm import select_scaled_mm_splits as splits
+
+    def auto(m, n, k):
+        tile = pick(m, n, k)
+        return tile, splits(m, n, k, tile)
+
+    assert auto(512, 5376, 5120) == ((2, 2, 4, 4, 4, 1), 3)     # 168 tiles -> 504 workgroups
+    assert auto(1040, 1536, 6144) == ((2, 2, 4, 4, 4, 1), 4)    # 108 tiles
+    assert auto(256, 12288, 4096) == ((2, 2, 4, 4, 4, 1), 2)    # 192 tiles
+    assert auto(1040, 1024, 5120) == ((1, 4, 4, 4, 2, 1), 3)    # 72 tiles of 128 x 128: 64 x 128, 136 tiles
+    assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
+    assert auto(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)    # short K: no split
+    assert auto(192, 1536, 6144) == ((8, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
+    assert auto(4096, 12288, 3072) == ((2, 2, 4, 4, 8, 1), 1)   # full grids never split
+    assert auto(16, 14336, 4096)[1] == 1
+    # a pinned tile the heuristic would not pick is never split by it
+    assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
+    for m in (65, 128, 200, 512, 1040, 2320):
+        for n in (1024, 1536, 4096, 12288):
+            for k in (4096, 6144, 16384):
+                tile = pick(m, n, k)
+                s = splits(m, n, k, tile)
+                assert 1 <= s <= 8 and (s == 1 or -(-k // 64) // s >= 16)
 
 
 def test_heuristic_returns_instantiated_tiles():
@@ -149,7 +227,8 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(4096, 12288, 3072) == (2, 2, 4, 4, 8, 1)   # C3: 3 full waves of 128 x 256
     assert pick(4096, 3072, 3072) == (2, 2, 4, 4, 4, 1)    # C2: one full wave of 128 x 128
     assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
-    assert pick(256, 12288, 4096) == (2, 2, 4, 2, 2, 1)    # small grid of 128 x 128: 64 x 64 ring
+    assert pick(4112, 1024, 5120) == (1, 4, 4, 4, 2, 1)    # one partial wave: 64 x 128 ring tiles
+    assert pick(2304, 1280, 1280) == (2, 2, 4, 2, 2, 1)    # small grid, short K: 64 x 64 ring
     assert pick(512, 1024, 1024) == (4, 1, 4, 1, 4, 0)     # tiny grid: streaming, 4 K slices
     assert pick(32, 25600, 5120) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
     assert pick(16, 14336, 4096) == (8, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 8 K slices

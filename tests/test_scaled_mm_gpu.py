@@ -137,7 +137,10 @@ HEURISTIC_CELLS = [
     (16, 6144, 6144),    # 16 x 32 columns
     (32, 25600, 5120),   # 32-row streaming tile
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
-    (256, 12288, 4096),  # 64 x 64 ring tile
+    (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
+    (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways
+    (2304, 1280, 1280),  # 64 x 64 ring tile
+    (4112, 1024, 5120),  # 64 x 128 ring tile, one partial wave
     (512, 1024, 1024),   # 4-slice streaming tile
     (9216, 2048, 2048),  # 128 x 128 (one full wave of blocks)
     (2320, 6144, 6144),  # 128 x 256
@@ -291,13 +294,14 @@ def test_op_rejects_bad_inputs(fo):
         fo.scaled_mm_hip(a, bp, None, torch.zeros(32, device="cuda", dtype=torch.bfloat16), torch.float16)
 
 
-def test_compile_matches_eager(fo):
+@pytest.mark.parametrize("n", [1024, 5376])  # 5376: the heuristic splits K (128 x 128 tiles, 3 ways)
+def test_compile_matches_eager(fo, n):
     """Reference tests/test_scaled_mm_hip_compile.py: one opaque node, eager == compiled."""
     for dynamic in (False, True):
         a = _tensor((512, 5120), torch.bfloat16)
-        bp = fo.prepack_b_for_scaled_mm(_tensor((5120, 1024), torch.float8_e5m2, seed=1))
+        bp = fo.prepack_b_for_scaled_mm(_tensor((5120, n), torch.float8_e5m2, seed=1))
         s = torch.tensor(2.34, device="cuda")
-        bias = _tensor((1024,), torch.bfloat16, seed=2)
+        bias = _tensor((n,), torch.bfloat16, seed=2)
 
         def run(a, bp, s, bias):
             return fo.scaled_mm_hip(a, bp, s, bias, torch.bfloat16)
