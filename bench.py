@@ -9,7 +9,8 @@ the kernels run on, bracketed by device synchronisation. value = TFLOP/s = 2*M*N
 
 Also reported: the skinny HBM-bound cell C4 (A fp16 [16, 4096] x W e5m2 [14336, 4096]) as GB/s of
 algorithmic bytes, timed over a HIP graph of launches that rotate over 8 distinct weight copies (8 x
-58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), and the CPU oracle
+58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2, a split-K
+cell (an underfilled grid, 512 x 5120 x 5376, with the best unsplit tile beside it), and the CPU oracle
 (oracle/scaled_mm_oracle.c, all host cores) on a row sample of C3 as `cpu_baseline`.
 
 Prints one JSON line (the driver's contract) on rank 0.
@@ -35,7 +36,7 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile without a
 # measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
-    ("c3", (2, 2, 4, 4, 8, 1)): (192379 * 2.0 + 101770 * 1.0) * 1024,
+    ("c3", (2, 2, 4, 4, 8, 1)): (196986 * 2.0 + 102631 * 1.0) * 1024,
     ("c4", (8, 1, 4, 1, 4, 0)): (29219 * 2.0 + 448 * 1.0) * 1024,
 }
 
@@ -158,6 +159,36 @@ def time_c2(steps: int = 100, warmup: int = 10):
     return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
 
 
+def time_splitk(steps: int = 100, warmup: int = 10):
+    """A split-K cell (fp16 [512, 5120] x e5m2 [5376, 5120] -> fp16: 168 tiles of 128 x 128 for 256 CUs),
+    TFLOP/s of the heuristic's pick (split along K) and of the best unsplit tile, timed the same way."""
+    import torch
+
+    import feather_ops
+    from feather_ops.scaled_mm import _launch, select_scaled_mm_splits
+
+    m, k, n = 512, 5120, 5376
+    a, bs, s = make_device_inputs(m, k, n, "fp16")
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    splits = select_scaled_mm_splits(m, n, k, tile)
+    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    res = {"tile": list(tile), "splits": splits}
+    for name, t, sp in (("auto", tile, splits), ("unsplit", (2, 2, 4, 2, 2, 1), 1)):
+        for _ in range(warmup):
+            _launch(a, bs[0], s, None, out, t, sp)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            _launch(a, bs[0], s, None, out, t, sp)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop) / steps
+        res[name] = {"us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    return res
+
+
 def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     """One kernel, `warmup + steps` eager launches, nothing else: the target of rocprofv3 --pmc runs.
 
@@ -226,7 +257,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 (HBM) and C2 (bf16) cells")
+    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 (HBM), C2 (bf16) and split-K cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()
@@ -248,6 +279,7 @@ def main() -> int:
     c3 = time_c3(args.steps, args.warmup)
     c4 = None if args.no_secondary else time_c4()
     c2 = None if args.no_secondary else time_c2()
+    sk = None if args.no_secondary else time_splitk()
     cpu = None if args.no_cpu else time_cpu_oracle()
 
     line = {
@@ -280,6 +312,11 @@ def main() -> int:
         line["bf16_cell"] = {"workload": "C2 DiT attention projection: bf16 [4096,3072] x e5m2 [3072,3072] -> bf16",
                              "TFLOPs": round(c2["tflops"], 1), "us_per_launch": round(c2["us"], 2),
                              "frac_fp16_peak": round(c2["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": c2["tile"]}
+    if sk is not None:
+        line["splitk_cell"] = {"workload": "underfilled grid: fp16 [512,5120] x e5m2 [5376,5120] -> fp16",
+                               "tile": sk["tile"], "splits": sk["splits"],
+                               "TFLOPs": round(sk["auto"]["tflops"], 1), "us_per_launch": round(sk["auto"]["us"], 2),
+                               "unsplit_64x64_TFLOPs": round(sk["unsplit"]["tflops"], 1)}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))
