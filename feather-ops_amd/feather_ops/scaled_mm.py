@@ -125,7 +125,9 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
 # Split-K workspaces, one per (device, stream): the counter area at their start must be zero before a
 # launch, and every completed launch leaves it zero whatever its shape, so a workspace is zeroed once, when
 # it is created, and then reused by the launches of its stream, which are ordered. Other streams get their
-# own.
+# own. Keys are stream handles: torch's streams come from per-device pools and are never destroyed, so a
+# handle is never reused for an unrelated stream (an external stream destroyed while work on it is pending
+# and recreated at the same address would break this; such streams should not share the cache).
 _split_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
