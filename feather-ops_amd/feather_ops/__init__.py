@@ -12,7 +12,13 @@ _lib.load()
 
 from .convert import bf16_to_fp16  # noqa: E402
 from .modules import relabel_modules, relabelled_class  # noqa: E402
-from .scaled_mm import prepack_b_for_scaled_mm, scaled_mm_hip, select_scaled_mm_config, tile_shape  # noqa: E402
+from .scaled_mm import (  # noqa: E402
+    prepack_b_for_scaled_mm,
+    scaled_mm_hip,
+    select_scaled_mm_config,
+    select_scaled_mm_splits,
+    tile_shape,
+)
 
 __all__ = [
     "bf16_to_fp16",
@@ -21,5 +27,6 @@ __all__ = [
     "relabelled_class",
     "scaled_mm_hip",
     "select_scaled_mm_config",
+    "select_scaled_mm_splits",
     "tile_shape",
 ]
