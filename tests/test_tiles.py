@@ -1,5 +1,5 @@
 """The tile table (reference tests/test_tiles.py): header current, heuristic aliases instantiated, no
-duplicates, and every tile fits gfx950's limits."""
+duplicates, every tile fits gfx950's limits, and every compiled kernel allocates exactly its tile's LDS."""
 
 import pathlib
 import subprocess
@@ -64,3 +64,39 @@ def test_tile_shape_formula():
 
     assert tile_shape((2, 4, 4, 8, 4, 1)) == (256, 256, 64)
     assert tile_shape((4, 1, 4, 1, 4, 0)) == (16, 64, 64)  # stream tiles split K across warps_m
+
+
+def _check_lds():
+    import importlib.util
+
+    path = pathlib.Path(__file__).resolve().parents[1] / "feather-ops_amd" / "check_lds.py"
+    spec = importlib.util.spec_from_file_location("_check_lds", path)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+def test_every_kernel_allocates_exactly_its_tiles_lds():
+    """The LDS audit (check_lds.py, the reference's tools/check_lds.py role): the compiled gfx950 code
+    object's group_segment_fixed_size of every ring (unsplit and split) and streaming instantiation equals
+    the size the tile asks for. Compiles one dtype combination (hipcc, device code only)."""
+    import pytest
+
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    check = _check_lds()
+    if not pathlib.Path(check.HIPCC).exists():
+        pytest.skip("needs hipcc")
+    asm = check.compile_asm("100")
+    checked, bad = check.audit(asm)
+    ring = sum(1 for t in SCALED_MM_TILES if t[5] == 1)
+    stream = len(SCALED_MM_TILES) - ring
+    assert checked == 2 * ring + stream
+    assert bad == []
+    # a planted off-by-one in the expectation is caught for every instantiation
+    real = check.expected_bytes
+    check.expected_bytes = lambda kernel, ints: real(kernel, ints) + 1
+    try:
+        assert len(check.audit(asm)[1]) == checked
+    finally:
+        check.expected_bytes = real
