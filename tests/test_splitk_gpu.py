@@ -148,6 +148,33 @@ def test_workspace_reuse_with_alternating_inputs(fo):
     assert int(counters.abs().sum().item()) == 0
 
 
+def test_concurrent_streams_use_their_own_workspaces(fo):
+    """Split launches on two streams at once: each stream has its own workspace, and both results are right."""
+    from feather_ops.scaled_mm import _split_workspaces
+
+    M, N, K = 512, 1536, 4096
+    tile = (2, 2, 4, 4, 4, 1)
+    inputs = [(_tensor((M, K), torch.float16, seed=40 + i),
+               fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=50 + i))) for i in range(2)]
+    want = [fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile) for a, bp in inputs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = [[], []]
+    for _ in range(4):
+        for i, stream in enumerate(streams):
+            with torch.cuda.stream(stream):
+                a, bp = inputs[i]
+                outs[i].append(fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile, splits=4))
+    torch.cuda.synchronize()
+    keys = {(torch.cuda.current_device(), s.cuda_stream) for s in streams}
+    assert keys <= set(_split_workspaces)
+    assert _split_workspaces[keys.pop()].data_ptr() != _split_workspaces[keys.pop()].data_ptr()
+    for i in range(2):
+        for out in outs[i]:
+            assert (out.float() - want[i].float()).abs().max().item() <= want[i].float().abs().max().item() * 2**-9
+    check_against_oracle(outs[1][-1], *inputs[1], None, None, rows=sample_rows(M))
+
+
 def test_graph_replay_matches_eager(fo):
     """Captured split launches replay correctly, with eager work and syncs between replays."""
     M, N, K = 256, 768, 2048
