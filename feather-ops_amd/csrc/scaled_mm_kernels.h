@@ -671,8 +671,10 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
                     // retires all reads of the slots refilled next (they held stage t - 1).
                     __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
                     barrier_only();
+                    __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
                     if (t + 1 < stages) load_a(t + 1);
                     if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                    __builtin_amdgcn_s_setprio(0);
                     compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
                     if (t + 1 < stages) commit_a((b + 1) % S::kSlotsA);
                 }
@@ -696,8 +698,13 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) v
                     // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
                     wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
                     barrier_only();
+                    // The refills go out at raised wave priority, so a wave that just passed its barrier
+                    // issues them ahead of the co-resident block's MFMAs (measured +1.6% on a 128 x 256 tile;
+                    // raising it for the MFMAs instead lost).
+                    __builtin_amdgcn_s_setprio(1);
                     if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
                     if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                    __builtin_amdgcn_s_setprio(0);
                     compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
                 }
             }
