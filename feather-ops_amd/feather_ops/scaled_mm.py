@@ -156,10 +156,14 @@ def _launch(
     if splits == 1:
         torch.ops.feather_ops.scaled_mm.default(a, b_prepacked, scale, bias, out, *tile)
         return
-    nbytes = split_workspace_bytes(a.shape[0], b_prepacked.shape[1], a.shape[1], tile, splits)
-    if nbytes < 0:
-        raise RuntimeError(f"split-K needs a ring tile and 1 <= splits <= the K stage count, got {tile}, {splits}")
-    ws = _split_workspace(a.device, nbytes)
+    if a.shape[0] == 0:  # an empty batch: the op checks its arguments and launches nothing
+        ws = torch.empty(0, dtype=torch.uint8, device=a.device)
+    else:
+        nbytes = split_workspace_bytes(a.shape[0], b_prepacked.shape[1], a.shape[1], tile, splits)
+        if nbytes < 0:
+            raise RuntimeError(
+                f"split-K needs a ring tile and 1 <= splits <= the K stage count, got {tile}, {splits}")
+        ws = _split_workspace(a.device, nbytes)
     torch.ops.feather_ops.scaled_mm_splitk.default(a, b_prepacked, scale, bias, out, ws, splits, *tile[:5])
 
 

@@ -309,3 +309,52 @@ def test_compile_matches_eager(fo, n):
         eager = run(a, bp, s, bias)
         compiled = torch.compile(run, fullgraph=True, dynamic=dynamic)(a, bp, s, bias)
         assert torch.equal(compiled.view(torch.int16), eager.view(torch.int16))
+
+
+# ---- empty and maximum sizes ----------------------------------------------------------------------------------
+
+def test_empty_m_returns_an_empty_output(fo):
+    """M = 0 (an empty batch): every entry point returns a [0, N] output and launches nothing."""
+    bp = fo.prepack_b_for_scaled_mm(_tensor((256, 128), torch.float8_e5m2, seed=1))
+    a = torch.empty((0, 256), dtype=torch.float16, device="cuda")
+    for kwargs in ({}, {"tile": (2, 2, 4, 4, 4, 1)}, {"tile": (8, 1, 4, 1, 4, 0)},
+                   {"tile": (2, 2, 4, 4, 4, 1), "splits": 2}):
+        out = fo.scaled_mm_hip(a, bp, torch.tensor(1.0, device="cuda"), None, torch.bfloat16, **kwargs)
+        assert out.shape == (0, 128) and out.dtype == torch.bfloat16
+    torch.cuda.synchronize()
+
+
+def test_output_just_under_2_gib(fo):
+    """The largest output the 31-bit buffer offsets allow: 65528 x 16384 fp16 (2,147,221,504 bytes), checked
+    on its first, last and sampled rows; one more row block is refused with the reference's message."""
+    M, N, K = 65528, 16384, 256
+    a = _tensor((M, K), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.05, device="cuda")
+    out = fo.scaled_mm_hip(a, bp, s, None, torch.float16)
+    check_against_oracle(out, a, bp, s, None, rows=sample_rows(M, n_random=16))
+    del out
+    torch.cuda.empty_cache()
+    a2 = _tensor((M + 8, K), torch.float16)
+    with pytest.raises(RuntimeError, match="smaller than 2 GiB"):
+        fo.scaled_mm_hip(a2, bp, s, None, torch.float16)
+
+
+def test_long_k(fo):
+    """K = 262144 (4096 stages of 64, a 256 MiB prepacked weight) through the ring and streaming kernels."""
+    K, N = 262144, 1024
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.02, device="cuda")
+    for m, tile in ((200, (2, 2, 4, 4, 4, 1)), (16, (8, 1, 4, 1, 4, 0))):
+        a = _tensor((m, K), torch.float16)
+        out = fo.scaled_mm_hip(a, bp, s, None, torch.float16, tile=tile)
+        check_against_oracle(out, a, bp, s, None, rows=sample_rows(m, n_random=8))
+
+
+def test_split_k_at_the_maximum_split_count(fo):
+    M, N, K = 130, 264, 2048  # 32 stages of 64: 32 splits of one stage each
+    a = _tensor((M, K), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    bias = _tensor((N,), torch.bfloat16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, None, bias, torch.bfloat16, tile=(2, 2, 4, 4, 4, 1), splits=32)
+    check_against_oracle(out, a, bp, None, bias)
