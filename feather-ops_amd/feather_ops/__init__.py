@@ -11,9 +11,10 @@ from . import _lib
 _lib.load()
 
 from .convert import bf16_to_fp16  # noqa: E402
-from .modules import relabel_modules, relabelled_class  # noqa: E402
+from .modules import ScaledMMLinear, relabel_modules, relabelled_class, to_scaled_mm_linear  # noqa: E402
 from .scaled_mm import (  # noqa: E402
     prepack_b_for_scaled_mm,
+    prepack_transpose,
     scaled_mm_hip,
     select_scaled_mm_config,
     select_scaled_mm_splits,
@@ -21,12 +22,15 @@ from .scaled_mm import (  # noqa: E402
 )
 
 __all__ = [
+    "ScaledMMLinear",
     "bf16_to_fp16",
     "prepack_b_for_scaled_mm",
+    "prepack_transpose",
     "relabel_modules",
     "relabelled_class",
     "scaled_mm_hip",
     "select_scaled_mm_config",
     "select_scaled_mm_splits",
     "tile_shape",
+    "to_scaled_mm_linear",
 ]

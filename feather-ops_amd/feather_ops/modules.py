@@ -9,6 +9,7 @@ mixin's `forward` does is the consumer's policy, passed in as `accept` and `mixi
 
 from collections.abc import Callable
 
+import torch
 from torch import nn
 
 # (original class, mixin) -> the relabelled class, so every relabel of the same pair yields one type object.
@@ -43,3 +44,54 @@ def relabel_modules(root: nn.Module, mixin: type, accept: Callable[[nn.Module], 
             module.__class__ = relabelled_class(type(module), mixin)
             changed += 1
     return changed
+
+
+_FP8_MAX = {torch.float8_e5m2: 57344.0, torch.float8_e4m3fn: 448.0}
+
+
+class ScaledMMLinear:
+    """Mixin for `nn.Linear` (via `relabel_modules`): `forward` runs the fp8 scaled matmul on a quantized
+    copy of the weight. Not in the reference, which leaves the Linear to its consumers; this is the
+    consumer-facing drop-in on top of `prepack_transpose`.
+
+    `quantize_weight_` (called by `to_scaled_mm_linear`) fills two non-persistent buffers, so `state_dict`
+    keys and values are unchanged: `weight_fp8` `[K_pad/16, N, 16]` and `weight_scale` (one fp32 value per
+    tensor, or N per output channel). Inputs are fp16 or bf16 `[..., in_features]`; the output has the
+    input's dtype.
+    """
+
+    def quantize_weight_(self, fp8_dtype: torch.dtype = torch.float8_e5m2, per_channel: bool = False) -> None:
+        from .scaled_mm import prepack_transpose
+
+        w = self.weight.detach().float()
+        amax = w.abs().amax(dim=1) if per_channel else w.abs().max().reshape(1)
+        scale = torch.where(amax > 0, amax / _FP8_MAX[fp8_dtype], torch.ones_like(amax))
+        wq = (w / (scale[:, None] if per_channel else scale)).to(fp8_dtype)
+        self.register_buffer("weight_fp8", prepack_transpose(wq), persistent=False)
+        self.register_buffer("weight_scale", scale.contiguous() if per_channel else scale.reshape(()),
+                             persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from .scaled_mm import scaled_mm_hip
+
+        bias = None if self.bias is None else self.bias.to(x.dtype)
+        x2 = x.reshape(-1, x.shape[-1])
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.clone(memory_format=torch.contiguous_format)  # the kernel reads 16-byte-aligned rows
+        y = scaled_mm_hip(x2, self.weight_fp8, self.weight_scale, bias, x.dtype)
+        return y.reshape(*x.shape[:-1], y.shape[-1])
+
+
+def to_scaled_mm_linear(root: nn.Module, fp8_dtype: torch.dtype = torch.float8_e5m2, per_channel: bool = False,
+                        accept: Callable[[nn.Module], bool] | None = None) -> int:
+    """Relabel the `nn.Linear` modules under `root` (those `accept` approves, by default every Linear whose
+    out_features is a multiple of 8 and in_features of 16, the kernel's contract) as `ScaledMMLinear` and
+    quantize their weights; return how many changed."""
+    def default_accept(module: nn.Module) -> bool:
+        return isinstance(module, nn.Linear) and module.out_features % 8 == 0 and module.in_features % 16 == 0
+
+    count = relabel_modules(root, ScaledMMLinear, accept or default_accept)
+    for module in root.modules():
+        if isinstance(module, ScaledMMLinear) and not hasattr(module, "weight_fp8"):
+            module.quantize_weight_(fp8_dtype, per_channel)
+    return count

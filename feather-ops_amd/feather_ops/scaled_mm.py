@@ -230,6 +230,23 @@ def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
     return b.view(k_pad // 16, 16, n).permute(0, 2, 1).contiguous()
 
 
+def prepack_transpose(w: torch.Tensor) -> torch.Tensor:
+    """`[N, K]` fp8 weight (an `nn.Linear` weight, out x in) -> `[K_pad/16, N, 16]`: the same layout as
+    `prepack_b_for_scaled_mm(w.t())` without materializing the transpose (the external consumer's
+    `comfy_feather/quant.py::prepack_transpose`, named at the reference's `scaled_mm.py:141-142`).
+
+    For a row of `w` the 16 k values of a chunk are already 16 contiguous bytes, so the prepack is a
+    transpose of `[N, K_pad/16]` 16-byte units.
+    """
+    n, k = w.shape
+    k_pad = -(-k // 128) * 128
+    if k_pad != k:
+        padded = torch.zeros((n, k_pad), device=w.device, dtype=w.dtype)
+        padded[:, :k] = w
+        w = padded
+    return w.view(n, k_pad // 16, 16).transpose(0, 1).contiguous()
+
+
 def tile_shape(tile: tuple[int, ...]) -> tuple[int, int, int]:
     """`(block_m, block_n, chunk_k)` of a tile."""
     return gemm_block_sizes(tile)
