@@ -57,7 +57,8 @@ class ScaledMMLinear:
     `quantize_weight_` (called by `to_scaled_mm_linear`) fills two non-persistent buffers, so `state_dict`
     keys and values are unchanged: `weight_fp8` `[K_pad/16, N, 16]` and `weight_scale` (one fp32 value per
     tensor, or N per output channel). Inputs are fp16 or bf16 `[..., in_features]`; the output has the
-    input's dtype.
+    input's dtype. The weight is frozen; gradients reach the input and the bias (computed in fp32 on the
+    dequantized weight), so the layer can sit under trainable adapters.
     """
 
     def quantize_weight_(self, fp8_dtype: torch.dtype = torch.float8_e5m2, per_channel: bool = False) -> None:
@@ -72,14 +73,51 @@ class ScaledMMLinear:
                              persistent=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        from .scaled_mm import scaled_mm_hip
-
         bias = None if self.bias is None else self.bias.to(x.dtype)
-        x2 = x.reshape(-1, x.shape[-1])
-        if not x2.is_contiguous() or x2.data_ptr() % 16:
-            x2 = x2.clone(memory_format=torch.contiguous_format)  # the kernel reads 16-byte-aligned rows
-        y = scaled_mm_hip(x2, self.weight_fp8, self.weight_scale, bias, x.dtype)
-        return y.reshape(*x.shape[:-1], y.shape[-1])
+        return _scaled_mm_linear(x, self.weight_fp8, self.weight_scale, bias)
+
+
+@torch.library.custom_op("feather_ops::scaled_mm_linear", mutates_args=())
+def _scaled_mm_linear(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale: torch.Tensor,
+                      bias: torch.Tensor | None) -> torch.Tensor:
+    """ScaledMMLinear's forward as one opaque op (like `feather_ops::scaled_mm_auto`), so `torch.compile`
+    traces neither the flattening nor the alignment check: `[..., K]` -> `[..., N]` in x's dtype."""
+    from .scaled_mm import scaled_mm_hip
+
+    x2 = x.reshape(-1, x.shape[-1])
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.clone(memory_format=torch.contiguous_format)  # the kernel reads 16-byte-aligned rows
+    y = scaled_mm_hip(x2, weight_fp8, weight_scale, bias, x.dtype)
+    return y.reshape(*x.shape[:-1], y.shape[-1])
+
+
+@_scaled_mm_linear.register_fake
+def _(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale: torch.Tensor,
+      bias: torch.Tensor | None) -> torch.Tensor:
+    return x.new_empty((*x.shape[:-1], weight_fp8.shape[1]))
+
+
+def _linear_setup_context(ctx, inputs, output) -> None:
+    x, weight_fp8, weight_scale, bias = inputs
+    ctx.save_for_backward(weight_fp8, weight_scale)
+    ctx.x_shape, ctx.x_dtype = x.shape, x.dtype
+    ctx.bias_dtype = None if bias is None else bias.dtype
+
+
+def _linear_backward(ctx, grad: torch.Tensor):
+    """Gradients for the activations and the bias (the fp8 weight is frozen): dX = dY @ (Wq * scale)^T in
+    fp32 on the dequantized weight, dbias = the column sums of dY."""
+    weight_fp8, weight_scale = ctx.saved_tensors
+    k = ctx.x_shape[-1]
+    chunks, n, _ = weight_fp8.shape
+    w = weight_fp8.permute(0, 2, 1).reshape(chunks * 16, n)[:k].float() * weight_scale.float()  # [K, N]
+    g = grad.reshape(-1, n).float()
+    grad_x = (g @ w.t()).to(ctx.x_dtype).reshape(ctx.x_shape)
+    grad_bias = None if ctx.bias_dtype is None else g.sum(0).to(ctx.bias_dtype)
+    return grad_x, None, None, grad_bias
+
+
+_scaled_mm_linear.register_autograd(_linear_backward, setup_context=_linear_setup_context)
 
 
 def to_scaled_mm_linear(root: nn.Module, fp8_dtype: torch.dtype = torch.float8_e5m2, per_channel: bool = False,

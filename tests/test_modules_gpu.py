@@ -67,3 +67,32 @@ def test_split_k_sized_layer(fo):
     x = torch.randn(512, 5120, device="cuda").to(torch.float16)
     y = lin(x)
     check_against_oracle(y, x, lin.weight_fp8, lin.weight_scale, lin.bias.to(torch.float16), rows=sample_rows(512))
+
+
+def test_compiled_model_matches_eager(fo):
+    """A model of ScaledMMLinear layers under torch.compile: the kernel stays one opaque node per layer."""
+    torch.manual_seed(3)
+    model = nn.Sequential(nn.Linear(512, 1024), nn.GELU(), nn.Linear(1024, 256)).cuda()
+    assert fo.to_scaled_mm_linear(model) == 2
+    x = torch.randn(4, 50, 512, device="cuda").to(torch.bfloat16)
+    eager = model(x)
+    compiled = torch.compile(model, fullgraph=True)(x)
+    assert torch.equal(compiled.view(torch.int16), eager.view(torch.int16))
+
+
+def test_backward_gives_input_and_bias_gradients(fo):
+    """dX = dY @ (Wq * scale)^T and dbias = sum(dY) on the dequantized weight; the fp8 weight is frozen."""
+    lin = _linear(256, 192)
+    fo.to_scaled_mm_linear(lin, torch.float8_e5m2, per_channel=True)
+    x = torch.randn(2, 30, 256, device="cuda").to(torch.bfloat16).requires_grad_()
+    y = lin(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    w = lin.weight_fp8.permute(0, 2, 1).reshape(-1, 192)[:256].float() * lin.weight_scale[None, :]
+    want_x = (g.reshape(-1, 192).float() @ w.t()).reshape(2, 30, 256)
+    assert x.grad.dtype == torch.bfloat16
+    assert torch.allclose(x.grad.float(), want_x.to(torch.bfloat16).float(), rtol=0, atol=0)
+    # the bias enters the op cast to the input dtype, so its gradient arrives through that cast (bf16)
+    want_bias = g.float().sum((0, 1))
+    assert torch.allclose(lin.bias.grad, want_bias, rtol=2**-7, atol=1e-3)
+    assert lin.weight.grad is None

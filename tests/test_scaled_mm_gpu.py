@@ -294,12 +294,14 @@ def test_op_rejects_bad_inputs(fo):
         fo.scaled_mm_hip(a, bp, None, torch.zeros(32, device="cuda", dtype=torch.bfloat16), torch.float16)
 
 
-@pytest.mark.parametrize("n", [1024, 5376])  # 5376: the heuristic splits K (128 x 128 tiles, 3 ways)
-def test_compile_matches_eager(fo, n):
+# The reference's compile shapes (tests/test_scaled_mm_hip_compile.py:7), plus one the heuristic splits K on
+# (512 x 5376 x 5120: 128 x 128 tiles, 3 ways).
+@pytest.mark.parametrize("m,n,k", [(4112, 1152, 1152), (512, 1024, 5120), (512, 5376, 5120)])
+def test_compile_matches_eager(fo, m, n, k):
     """Reference tests/test_scaled_mm_hip_compile.py: one opaque node, eager == compiled."""
     for dynamic in (False, True):
-        a = _tensor((512, 5120), torch.bfloat16)
-        bp = fo.prepack_b_for_scaled_mm(_tensor((5120, n), torch.float8_e5m2, seed=1))
+        a = _tensor((m, k), torch.bfloat16)
+        bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
         s = torch.tensor(2.34, device="cuda")
         bias = _tensor((n,), torch.bfloat16, seed=2)
 
