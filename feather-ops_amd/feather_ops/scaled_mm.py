@@ -16,6 +16,8 @@ opaque custom op, so `torch.compile` sees one node whatever the shape (reference
 Pass `tile=` to pin it, which is what the benchmark sweeps and the tests do.
 """
 
+import functools
+
 import torch
 from torch.library import custom_op
 
@@ -122,6 +124,14 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
     return max(2, min(8, (2 * _CUS) // _blocks(M, N, tile), stages // _SPLIT_MIN_STAGES))
 
 
+@functools.lru_cache(maxsize=4096)
+def _auto_choice(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int, int], int]:
+    """(tile, splits) the heuristic picks for a shape, memoized: a model runs the same few shapes again
+    and again, and the auto path then skips the model arithmetic (1-5 us of Python per call)."""
+    tile = select_scaled_mm_config(M, N, K)
+    return tile, select_scaled_mm_splits(M, N, K, tile)
+
+
 # Split-K workspaces, one per (device, stream): the counter area at their start must be zero before a
 # launch, and every completed launch leaves it zero whatever its shape, so a workspace is zeroed once, when
 # it is created, and then reused by the launches of its stream, which are ordered. Other streams get their
@@ -176,9 +186,7 @@ def _scaled_mm_auto(
     out: torch.Tensor,
 ) -> None:
     """The heuristic behind an opaque boundary: `torch.compile` does not specialize on its branches."""
-    M, N, K = a.shape[0], b_prepacked.shape[1], a.shape[1]
-    tile = select_scaled_mm_config(M, N, K, a.dtype, b_prepacked.dtype, out.dtype)
-    _launch(a, b_prepacked, scale, bias, out, tile, select_scaled_mm_splits(M, N, K, tile))
+    _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1]))
 
 
 def scaled_mm_hip(
