@@ -2,6 +2,7 @@
 //
 //   c[m, n] = round_out( fp32( sum_k fp16(a[m, k]) * fp16(B[k, n]) ) * scale ) (+ bias[n], in out precision)
 //   B[k, n] = b_prepacked[k / 16][n][k % 16]                 (feather_ops/scaled_mm.py:137-150)
+// with `scale` one value per tensor or one per output column n (naive.py:29-33).
 //
 // Semantics follow the reference's naive path (feather_ops/naive.py:4-41) with fp32 accumulation:
 // bf16 activations are widened to fp16 with round-to-nearest-even (naive.py:21), the weight byte is
@@ -11,12 +12,14 @@
 //
 // Two kernel families share the fragment layout, the decode and the epilogue:
 //  - ring_dma_kernel (tile field prefetch = 1): a block owns a BM x BN output tile, waves split it WM x WN,
-//                  and K streams through an LDS ring of 16*U-deep stages (2 or 3 buffers). Activation and
-//                  weight tiles go from HBM straight into LDS with buffer loads that write LDS (no VGPR
-//                  staging); the next stages are in flight while the current one feeds the MFMAs. bf16
-//                  activations travel as they are and are widened to fp16 per fragment after the LDS read.
-//  - stream_kernel (prefetch = 0): for skinny M. No LDS staging: each wave streams its fragments
-//                  straight from global memory into VGPRs (register double buffer), the block's WM
+//                  and K streams through separate activation and weight LDS rings of 16*U-deep stages.
+//                  The tiles go from HBM straight into LDS with buffer loads that write LDS; the next
+//                  stages are in flight while the current one feeds the MFMAs. bf16 activations are
+//                  staged through registers and widened to fp16 once per block in 4-wave blocks, per
+//                  fragment after the LDS read in 8-wave blocks. A separate instantiation splits each
+//                  tile's K range over several workgroups whose partial sums meet in a workspace.
+//  - stream_kernel (prefetch = 0): for skinny M. Weights stream from HBM straight into VGPRs (register
+//                  double buffer), activations through a small per-wave LDS double buffer; the block's WM
 //                  waves split K, and a short LDS reduction joins their fp32 partial sums.
 //
 // Fragment layout (v_mfma_f32_16x16x32_f16, wave64). The MFMA's first operand (16 "rows" i) carries 16
