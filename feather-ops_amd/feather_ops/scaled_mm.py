@@ -154,6 +154,15 @@ def _split_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def clear_split_workspaces() -> None:
+    """Release the cached split-K workspaces (they are recreated, zeroed, on the next split launch).
+
+    Call it only when no split launch is still running on the streams whose workspaces are dropped, e.g.
+    after `torch.cuda.synchronize()`; the memory returns to torch's caching allocator.
+    """
+    _split_workspaces.clear()
+
+
 def _launch(
     a: torch.Tensor,
     b_prepacked: torch.Tensor,

@@ -175,6 +175,21 @@ def test_concurrent_streams_use_their_own_workspaces(fo):
     check_against_oracle(outs[1][-1], *inputs[1], None, None, rows=sample_rows(M))
 
 
+def test_cleared_workspaces_are_recreated_zeroed(fo):
+    from feather_ops.scaled_mm import _split_workspaces, clear_split_workspaces
+
+    M, N, K = 256, 512, 4096
+    a = _tensor((M, K), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    first = fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=(2, 2, 4, 4, 4, 1), splits=4)
+    torch.cuda.synchronize()
+    clear_split_workspaces()
+    assert not _split_workspaces
+    again = fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=(2, 2, 4, 4, 4, 1), splits=4)
+    assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+    assert _split_workspaces
+
+
 def test_graph_replay_matches_eager(fo):
     """Captured split launches replay correctly, with eager work and syncs between replays."""
     M, N, K = 256, 768, 2048
