@@ -16,10 +16,14 @@ Run from `feather-ops_amd/`:
     python -m benchmarks.benchmark_scaled_mm_hip --tiles "2,2,4,4,8,1;8,1,4,1,4,0"
     python -m benchmarks.benchmark_scaled_mm_hip --cells "4096,12288,3072" --cold
     python -m benchmarks.benchmark_scaled_mm_hip --tiles --splits 2,3,4,6,8   # split-K candidates too
+    python -m benchmarks.benchmark_scaled_mm_hip --groups text-16 --graph      # kernel time, no host gaps
 
-`auto` is the whole heuristic (tile and split count). With `--splits`, every listed ring tile whose grid
-has fewer tiles than the GPU has compute units is also timed split `S` ways (named `(tile)/S`), for each
-`S` that keeps at most four workgroups per CU.
+`auto` is the whole heuristic (tile and split count). With `--splits`, every listed tile (ring or
+streaming) whose grid has fewer tiles than the GPU has compute units is also timed split `S` ways (named
+`(tile)/S`), for each `S` that keeps at most four workgroups per CU. Every provider calls its op directly
+(split launches with one preallocated workspace per cell), so the Python layer's per-call cost is not
+timed; `--graph` also takes the op dispatch out (replays of captured batches), which matters for kernels
+of a few microseconds.
 """
 
 import argparse
@@ -35,7 +39,6 @@ sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
 from benchmarks.cells import GROUPS, cells  # noqa: E402
 from benchmarks.protocol import measure, paired_speedup  # noqa: E402
 from feather_ops.scaled_mm import (  # noqa: E402
-    _launch,
     prepack_b_for_scaled_mm,
     select_scaled_mm_config,
     select_scaled_mm_splits,
@@ -43,6 +46,11 @@ from feather_ops.scaled_mm import (  # noqa: E402
 from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, split_workspace_bytes  # noqa: E402
 
 _CUS = 256
+
+
+def _blocks(m: int, n: int, tile: tuple[int, ...]) -> int:
+    bm, bn, _ = gemm_block_sizes(tile)
+    return -(-m // bm) * -(-n // bn)
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}
 
@@ -88,21 +96,31 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
 
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, out_dtype))
     picked_splits = select_scaled_mm_splits(m, n, k, picked)
+    split_cases = [(tile, splits) for tile in tiles for splits in args.splits
+                   if _blocks(m, n, tile) < _CUS and _blocks(m, n, tile) * splits <= 4 * _CUS
+                   and split_workspace_bytes(m, n, k, tile, splits) > 0]
+    if picked_splits > 1:
+        split_cases.append((picked, picked_splits))
+    # One zeroed workspace for every split launch of the cell (each leaves its counters at zero), passed
+    # to the op directly, so that a launch allocates nothing and can be captured.
+    ws_bytes = max([split_workspace_bytes(m, n, k, tile, splits) for tile, splits in split_cases], default=0)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    split_op = torch.ops.feather_ops.scaled_mm_splitk.default
+
+    def launcher(tile, splits):
+        if splits == 1:
+            return lambda i: op(a, packs[i % copies], scale, bias, out, *tile)
+        return lambda i: split_op(a, packs[i % copies], scale, bias, out, ws, splits, *tile)
+
     providers = {"torch_mm": lambda i: torch.mm(control_a, control_w.t())}
     for tile in tiles:
-        providers[str(tile)] = lambda i, tile=tile: op(a, packs[i % copies], scale, bias, out, *tile)
-        if tile[5] != 1:
-            continue
-        bm, bn, _ = gemm_block_sizes(tile)
-        grid = -(-m // bm) * -(-n // bn)
-        for splits in args.splits:
-            if grid < _CUS and grid * splits <= 4 * _CUS and split_workspace_bytes(m, n, k, tile, splits) > 0:
-                providers[f"{tile}/{splits}"] = lambda i, tile=tile, splits=splits: _launch(
-                    a, packs[i % copies], scale, bias, out, tile, splits)
+        providers[str(tile)] = launcher(tile, 1)
+    for tile, splits in split_cases:
+        providers[f"{tile}/{splits}"] = launcher(tile, splits)
     auto_name = str(picked) if picked_splits == 1 else f"{picked}/{picked_splits}"
     if auto_name not in providers:  # when the sweep includes the pick, `auto` is that measurement
-        providers["auto"] = lambda i: _launch(a, packs[i % copies], scale, bias, out, picked, picked_splits)
-    res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms)
+        providers["auto"] = launcher(picked, picked_splits)
+    res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms, graph=args.graph)
     if "auto" not in res:
         res["auto"] = res[auto_name]
     tflops = {name: 2.0 * m * n * k / (r.median_ms * 1e-3) / 1e12 for name, r in res.items()}
@@ -124,7 +142,7 @@ def main() -> int:
     parser.add_argument("--groups", default="", help=f"comma-separated groups of cells.py: {','.join(GROUPS)}")
     parser.add_argument("--square", action="store_true", help="N^3 for N in 512..8192 instead of the grid")
     parser.add_argument("--tiles", nargs="?", const="", default=None, help="'m,n,u,rm,rn,p;...', or nothing for all")
-    parser.add_argument("--splits", default="", help="'2,3,4': split-K counts to time for underfilled ring grids")
+    parser.add_argument("--splits", default="", help="'2,3,4': split-K counts to time for underfilled grids")
     parser.add_argument("--a-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--out-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--no-bias", dest="bias", action="store_false")
@@ -132,6 +150,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--rounds", type=int, default=5)
     parser.add_argument("--target-ms", type=float, default=20.0)
+    parser.add_argument("--graph", action="store_true",
+                        help="time replays of captured batches (kernel time without host launch overhead)")
     parser.add_argument("--json", dest="json_path", default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():

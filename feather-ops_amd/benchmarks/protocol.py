@@ -5,9 +5,14 @@ stream; a case times every provider once per round, in an order rotated by one e
 on the box (5-10% between runs, and within a run while the part heats) hits every provider alike. The
 batch size comes from a single-launch estimate so that one batch takes about `target_ms`.
 
+With `graph=True` each provider's batch is captured once into a HIP graph and a measurement is one replay:
+the launches then follow each other without the host in between, so a kernel shorter than its launch
+path on the host (Python, op dispatch: 5-15 us) is timed by itself. Eager batches time what an eager
+caller sees, host overhead included when the kernel is shorter than it.
+
 Cold weights: on MI355X the 256 MB MALL holds most weights, so an L2 flush does not make a launch cold.
 A case instead rotates its weight over enough copies that they do not fit in the MALL (see
-`benchmark_scaled_mm_hip.py --rotate`), which is also what a model does when every layer has its own
+`benchmark_scaled_mm_hip.py --cold`), which is also what a model does when every layer has its own
 weight.
 """
 
@@ -61,24 +66,60 @@ def _batch_ms(fn: Callable[[int], object], start: int, iters: int) -> float:
     return begin.elapsed_time(end) / iters
 
 
+def _capture(fn: Callable[[int], object], iters: int) -> torch.cuda.CUDAGraph:
+    """A graph of `iters` launches of `fn` (indices 0 .. iters - 1), captured on a side stream."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            fn(i)
+    torch.cuda.synchronize()
+    return graph
+
+
+def _replay_ms(graph: torch.cuda.CUDAGraph, iters: int) -> float:
+    begin = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    begin.record()
+    graph.replay()
+    end.record()
+    end.synchronize()
+    return begin.elapsed_time(end) / iters
+
+
 def measure(providers: dict[str, Callable[[int], object]], *, warmup: int = 5, rounds: int = 5,
-            target_ms: float = 20.0, max_iters: int = 64) -> dict[str, Measurement]:
+            target_ms: float = 20.0, max_iters: int = 64, graph: bool = False) -> dict[str, Measurement]:
     """Time each provider (called with a running launch index, which a provider may use to rotate its
-    weight copies) over `rounds` interleaved rounds."""
+    weight copies) over `rounds` interleaved rounds; with `graph`, as replays of a captured batch of
+    `max_iters` launches."""
     names = list(providers)
     for name in names:
         for i in range(warmup):
             providers[name](i)
     torch.cuda.synchronize()
     iters = {}
+    graphs = {}
     for name in names:
-        one = max(_batch_ms(providers[name], 0, 1), 1e-4)
-        iters[name] = int(min(max(round(target_ms / one), 1), max_iters))
+        if graph:
+            iters[name] = max_iters
+            graphs[name] = _capture(providers[name], max_iters)
+            _replay_ms(graphs[name], max_iters)  # warm replay
+        else:
+            one = max(_batch_ms(providers[name], 0, 1), 1e-4)
+            iters[name] = int(min(max(round(target_ms / one), 1), max_iters))
     samples: dict[str, list[float]] = {name: [] for name in names}
     counter = 0
     for order in rotated_orders(names, rounds):
         for name in order:
-            samples[name].append(_batch_ms(providers[name], counter, iters[name]))
+            if graph:
+                samples[name].append(_replay_ms(graphs[name], iters[name]))
+            else:
+                samples[name].append(_batch_ms(providers[name], counter, iters[name]))
             counter += iters[name]
     return {name: Measurement.of(v) for name, v in samples.items()}
 

@@ -147,13 +147,13 @@ void scaled_mm(const Tensor& a, const Tensor& b_prepacked, const std::optional<T
     check_launch(launched, "scaled_mm");
 }
 
-// feather_ops::scaled_mm_splitk: scaled_mm on a ring-kernel tile with each tile's K range split over
+// feather_ops::scaled_mm_splitk: scaled_mm with each tile's K range split over
 // `splits` workgroups that meet in `workspace` (uint8, the caller's; all zero before its first use, and
 // every completed call leaves it reusable; see feather_scaled_mm_splitk). No counterpart in the reference.
 void scaled_mm_splitk(const Tensor& a, const Tensor& b_prepacked, const std::optional<Tensor>& scale,
                       const std::optional<Tensor>& bias, Tensor& c, Tensor& workspace, const int64_t splits,
                       const int64_t block_warps_m, const int64_t block_warps_n, const int64_t unroll_k,
-                      const int64_t repeat_m, const int64_t repeat_n) {
+                      const int64_t repeat_m, const int64_t repeat_n, const bool prefetch) {
     const Operands o = check_operands(a, b_prepacked, scale, bias, c, block_warps_m, block_warps_n);
     STD_TORCH_CHECK(workspace.is_cuda() && workspace.get_device_index() == o.device_index,
                     "workspace must be on the same device as a");
@@ -164,7 +164,7 @@ void scaled_mm_splitk(const Tensor& a, const Tensor& b_prepacked, const std::opt
     const int64_t need = feather_splitk_workspace_bytes(o.M, o.N, o.K, static_cast<int>(block_warps_m),
                                                         static_cast<int>(block_warps_n), static_cast<int>(unroll_k),
                                                         static_cast<int>(repeat_m), static_cast<int>(repeat_n),
-                                                        static_cast<int>(splits));
+                                                        prefetch, static_cast<int>(splits));
     STD_TORCH_CHECK(need >= 0, "Unsupported config");
     STD_TORCH_CHECK(splits == 1 || workspace.numel() >= need, "workspace must hold at least ", need, " bytes");
     STD_TORCH_CHECK(splits == 1 || is_aligned(workspace.const_data_ptr(), 256),
@@ -176,8 +176,8 @@ void scaled_mm_splitk(const Tensor& a, const Tensor& b_prepacked, const std::opt
         bias.has_value() ? static_cast<const uint16_t*>(bias->const_data_ptr()) : nullptr,
         static_cast<uint16_t*>(c.mutable_data_ptr()), o.M, o.N, o.K, o.scale_mode, bias.has_value() ? 1 : 0, o.e5m2,
         o.a_bf16, o.out_bf16, static_cast<int>(block_warps_m), static_cast<int>(block_warps_n),
-        static_cast<int>(unroll_k), static_cast<int>(repeat_m), static_cast<int>(repeat_n), static_cast<int>(splits),
-        workspace.mutable_data_ptr(), workspace.numel(), current_stream(o.device_index));
+        static_cast<int>(unroll_k), static_cast<int>(repeat_m), static_cast<int>(repeat_n), prefetch,
+        static_cast<int>(splits), workspace.mutable_data_ptr(), workspace.numel(), current_stream(o.device_index));
     check_launch(launched, "scaled_mm_splitk");
 }
 
@@ -245,7 +245,7 @@ STABLE_TORCH_LIBRARY(feather_ops, m) {
     m.def(
         "scaled_mm_splitk(Tensor a, Tensor b_prepacked, Tensor? scale, Tensor? bias, Tensor(a!) c, "
         "Tensor(b!) workspace, int splits, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, "
-        "int repeat_n) -> ()");
+        "int repeat_n, bool prefetch=True) -> ()");
     m.def("bf16_to_fp16(Tensor x, Tensor(a!) out) -> ()");
     m.def("prepack_b(Tensor b, Tensor(a!) out) -> ()");
 }

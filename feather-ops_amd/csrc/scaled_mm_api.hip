@@ -36,36 +36,40 @@ bool contract_ok(const uint16_t* a, const uint8_t* b, const float* scale, const 
     return true;
 }
 
-// True for a ring-kernel (prefetch = 1) tile of the instantiated table: the only kernel that splits K.
-bool is_ring_tile(int wm, int wn, int u, int rm, int rn) {
-#define FEATHER_IS_RING_TILE(twm, twn, tu, trm, trn, tpf) \
-    || ((tpf) != 0 && wm == (twm) && wn == (twn) && u == (tu) && rm == (trm) && rn == (trn))
-    return false FEATHER_SCALED_MM_TILES(FEATHER_IS_RING_TILE);
-#undef FEATHER_IS_RING_TILE
+// True for a tile of the instantiated table.
+bool is_tile(int wm, int wn, int u, int rm, int rn, bool prefetch) {
+#define FEATHER_IS_TILE(twm, twn, tu, trm, trn, tpf) \
+    || (((tpf) != 0) == prefetch && wm == (twm) && wn == (twn) && u == (tu) && rm == (trm) && rn == (trn))
+    return false FEATHER_SCALED_MM_TILES(FEATHER_IS_TILE);
+#undef FEATHER_IS_TILE
 }
 
-// Workspace of a split launch: the counter area (one uint32 per tile and wave, at most kSplitCtrBytes), then
-// the partial sums (splits fp32 tiles per output tile); none for splits = 1. -1 when the tile, the split
-// count or the grid is out of contract.
+// Workspace of a split launch: the counter area (one uint32 per tile and join slot, at most kSplitCtrBytes),
+// then the partial sums (splits fp32 tiles per output tile); none for splits = 1. -1 when the tile, the
+// split count or the grid is out of contract. A ring tile joins per wave (WM * WN slots) and splits its
+// 16*U-deep stages; a streaming tile (block BM = 16 * RM, BN = 16 * WN * RN) joins per 16 x 16 fragment
+// (WN * RM * RN slots; WN when its block has one K slice) and splits its 64-deep groups.
 struct SplitLayout {
     int64_t ctr_bytes = -1;
     int64_t total_bytes = -1;
 };
 
-SplitLayout split_layout(int64_t M, int64_t N, int64_t K, int wm, int wn, int u, int rm, int rn, int splits) {
+SplitLayout split_layout(int64_t M, int64_t N, int64_t K, int wm, int wn, int u, int rm, int rn, bool prefetch,
+                         int splits) {
     SplitLayout l;
-    if (M < 1 || N < 1 || K < 16 || !is_ring_tile(wm, wn, u, rm, rn)) return l;
-    const int64_t stages = (K + 16 * u - 1) / (16 * u);
-    if (splits < 1 || splits > kMaxSplits || splits > stages) return l;
+    if (M < 1 || N < 1 || K < 16 || !is_tile(wm, wn, u, rm, rn, prefetch)) return l;
+    const int64_t units = prefetch ? (K + 16 * u - 1) / (16 * u) : (K + 63) / 64;
+    if (splits < 1 || splits > kMaxSplits || splits > units) return l;
     if (splits == 1) {  // the unsplit kernel: no workspace
         l.ctr_bytes = 0;
         l.total_bytes = 0;
         return l;
     }
-    const int64_t bm = 16 * wm * rm;
+    const int64_t bm = prefetch ? 16 * wm * rm : 16 * rm;
     const int64_t bn = 16 * wn * rn;
+    const int64_t slots = prefetch ? wm * wn : (wm > 1 ? wn * rm * rn : wn);
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    if (tiles * wm * wn * 4 > kSplitCtrBytes) return l;
+    if (tiles * slots * 4 > kSplitCtrBytes) return l;
     const int64_t total = kSplitCtrBytes + tiles * splits * bm * bn * 4;
     if (total > kMaxBufferBytes) return l;
     l.ctr_bytes = kSplitCtrBytes;
@@ -124,8 +128,9 @@ extern "C" bool launch_scaled_mm(const uint16_t* const a, const uint8_t* const b
 extern "C" int64_t feather_splitk_workspace_bytes(const int64_t M, const int64_t N, const int64_t K,
                                                   const int block_warps_m, const int block_warps_n,
                                                   const int unroll_k, const int repeat_m, const int repeat_n,
-                                                  const int splits) {
-    return feather::split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, splits)
+                                                  const bool prefetch, const int splits) {
+    return feather::split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch,
+                                 splits)
         .total_bytes;
 }
 
@@ -134,12 +139,13 @@ extern "C" bool feather_scaled_mm_splitk(const uint16_t* const a, const uint8_t*
                                          const int64_t M, const int64_t N, const int64_t K, const int has_scale,
                                          const int has_bias, const bool use_fp8_e5m2, const bool a_bf16,
                                          const bool output_bf16, const int block_warps_m, const int block_warps_n,
-                                         const int unroll_k, const int repeat_m, const int repeat_n, const int splits,
-                                         void* const workspace, const int64_t workspace_bytes, hipStream_t stream) {
+                                         const int unroll_k, const int repeat_m, const int repeat_n,
+                                         const bool prefetch, const int splits, void* const workspace,
+                                         const int64_t workspace_bytes, hipStream_t stream) {
     using namespace feather;
     if (!contract_ok(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias)) return false;
     const SplitLayout l =
-        split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, splits);
+        split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch, splits);
     if (l.total_bytes < 0) return false;
     if (splits > 1 && (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total_bytes)) return false;
     Params p = make_params(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias);
@@ -148,6 +154,6 @@ extern "C" bool feather_scaled_mm_splitk(const uint16_t* const a, const uint8_t*
         p.split_ctr = static_cast<uint32_t*>(workspace);
         p.split_part = static_cast<uint8_t*>(workspace) + l.ctr_bytes;
     }
-    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, true};
+    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
     return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);
 }

@@ -20,7 +20,8 @@
 //                  tile's K range over several workgroups whose partial sums meet in a workspace.
 //  - stream_kernel (prefetch = 0): for skinny M. Weights stream from HBM straight into VGPRs (register
 //                  double buffer), activations through a small per-wave LDS double buffer; the block's WM
-//                  waves split K, and a short LDS reduction joins their fp32 partial sums.
+//                  waves split K, and a short LDS reduction joins their fp32 partial sums. A separate
+//                  instantiation also splits each tile's K range over workgroups, joined per fragment.
 //
 // Fragment layout (v_mfma_f32_16x16x32_f16, wave64). The MFMA's first operand (16 "rows" i) carries 16
 // weight columns and its second operand (16 "columns" j) carries 16 activation rows, so each lane ends
@@ -314,21 +315,23 @@ __device__ __forceinline__ void tile_of_block(int bid, int nblocks, int tiles_m,
 // bit the compiler itself sets for relaxed agent-scope atomic loads and stores.)
 constexpr int kDeviceScope = 16;
 
-// One wave's side of the split-K join, after its K range is accumulated. The wave parks its partial sums in
-// its slot of the workspace with device-coherent stores, waits until they are written, and counts itself in
-// at its (tile, wave) counter. The last of the tile's `splits` waves to arrive reads every partial back,
+// One wave's side of the split-K join, after its K range is accumulated. A tile joins in kSlots independent
+// parts (the ring kernel: one per wave's sub-tile; the streaming kernel: one per 16 x 16 fragment), and the
+// wave holds part `slot`. It parks its partial sums in that part's place in the workspace with
+// device-coherent stores, waits until they are written, and counts itself in at the (tile, slot) counter.
+// The last of the part's `splits` waves to arrive reads every partial back,
 // adds them in split order 0, 1, ..., splits - 1 (the same order whichever arrives last, so results are
 // deterministic), resets the counter to zero for the next launch and returns true: it then stores the tile.
 // The others return false and end. No wave ever waits for another workgroup, so the join cannot stall
 // whatever the dispatch order. Agent-scope fences would do instead of the coherent accesses, but they write
 // back and invalidate the whole L2 of the XCD under every co-resident workgroup (measured 1.5-2x slower).
-template <int kWaves, int RM, int RN>
-__device__ __forceinline__ bool join_split(const Params& p, f32x4 (&acc)[RM][RN], int tile_id, int split, int wave,
+template <int kSlots, int RM, int RN>
+__device__ __forceinline__ bool join_split(const Params& p, f32x4 (&acc)[RM][RN], int tile_id, int split, int slot_id,
                                            int lane) {
     constexpr uint32_t kSlotBytes = RM * RN * kWave * 16;
     const rsrc_t part = make_rsrc(p.split_part, 0x7fffffffu);
     const auto slot = [&](int s) {
-        return (static_cast<uint32_t>(tile_id * p.splits + s) * kWaves + static_cast<uint32_t>(wave)) * kSlotBytes +
+        return (static_cast<uint32_t>(tile_id * p.splits + s) * kSlots + static_cast<uint32_t>(slot_id)) * kSlotBytes +
                static_cast<uint32_t>(lane) * 16u;
     };
 #pragma unroll
@@ -340,7 +343,7 @@ __device__ __forceinline__ bool join_split(const Params& p, f32x4 (&acc)[RM][RN]
     // The stores must be complete (visible at device scope) before the counter says so; the memory clobber
     // keeps the compiler from moving the atomic above them.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t* ctr = p.split_ctr + tile_id * kWaves + wave;
+    uint32_t* ctr = p.split_ctr + tile_id * kSlots + slot_id;
     uint32_t arrived = 0;
     if (lane == 0) arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     arrived = __builtin_amdgcn_readfirstlane(arrived);
@@ -747,7 +750,7 @@ struct StreamShape {
     static_assert(kLoadsPerFetch < 64, "vmcnt range");
 };
 
-template <int KS, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16>
+template <int KS, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK>
 __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p) {
     using S = StreamShape<KS, WN, U, RM, RN>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
@@ -760,8 +763,12 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
 
     const float scale = load_scale(p);
     const int tiles_n = (p.N + S::kBN - 1) / S::kBN;
-    const int tm = blockIdx.x / tiles_n;
-    const int tn = blockIdx.x % tiles_n;
+    // A split launch runs `splits` workgroups per tile, split-major (as the ring kernel's split launch).
+    const int n_tiles = ((p.M + S::kBM - 1) / S::kBM) * tiles_n;
+    const int split = kSplitK ? static_cast<int>(blockIdx.x) / n_tiles : 0;
+    const int tile_id = static_cast<int>(blockIdx.x) - split * n_tiles;
+    const int tm = tile_id / tiles_n;
+    const int tn = tile_id % tiles_n;
     const int m0 = tm * S::kBM;
     const int n0 = tn * S::kBN + wave_n * 16 * RN;
 
@@ -774,6 +781,12 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
     const int r16 = lane & 15;
     const int k_chunks = p.K / 16;
     const int groups_total = (k_chunks + 3) / 4;   // 64-deep groups covering K
+    // This workgroup's groups [group0, group_end): all of them, or its split's share. Chunks from chunk_end
+    // on read as zeros (the end of K, or the next split's range).
+    const int splits = kSplitK ? p.splits : 1;
+    const int group0 = split * groups_total / splits;
+    const int group_end = (split + 1) * groups_total / splits;
+    const int chunk_end = kSplitK ? min(k_chunks, 4 * group_end) : k_chunks;
 
     // Activation fragments reach this wave's LDS buffer by direct loads of whole 128-byte row segments
     // (one instruction: 8 rows x 8 units of 16 bytes, unit = 8 consecutive k), so every cache line an
@@ -818,10 +831,10 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
         __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
 #pragma unroll
         for (int q = 0; q < S::kGroups; ++q) {
-            const int group = (it * S::kGroups + q) * KS + ks;   // K slices interleave group by group
+            const int group = group0 + (it * S::kGroups + q) * KS + ks;   // K slices interleave group by group
             const uint32_t a_soff = static_cast<uint32_t>(group) * 128u;
             uint8_t* const dst = a_lds + buf * S::kABufBytes + q * RM * S::kAFragBytes;
-            if (4 * group + 3 < k_chunks) {
+            if (4 * group + 3 < chunk_end) {
 #pragma unroll
                 for (int i = 0; i < RM; ++i)
 #pragma unroll
@@ -832,12 +845,12 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
                 for (int i = 0; i < RM; ++i)
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const bool ok = 4 * group + a_dma_chunk[h] < k_chunks;
+                        const bool ok = 4 * group + a_dma_chunk[h] < chunk_end;
                         dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, ok ? a_dma[i][h] : kOob, a_soff);
                     }
             }
             const int chunk = 4 * group + g;
-            const bool in_k = chunk < k_chunks;
+            const bool in_k = chunk < chunk_end;
 #pragma unroll
             for (int j = 0; j < RN; ++j) {
                 const uint32_t off = (b_base[j] == kOob || !in_k)
@@ -885,7 +898,7 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
     // while iteration it computes. Before a consume, this wave's loads of that iteration have landed
     // (vector-memory operations retire in issue order, so only the newer fetch may stay outstanding).
     const int per_iter = S::kGroups * KS;
-    const int iters = (groups_total + per_iter - 1) / per_iter;
+    const int iters = (group_end - group0 + per_iter - 1) / per_iter;
     Frag f0, f1;
     if (iters > 0) fetch(f0, 0, 0);
     int it = 0;
@@ -928,6 +941,10 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             f32x4 sum[1][1] = {{red[f * kWave + lane]}};
 #pragma unroll
             for (int k2 = 1; k2 < KS; ++k2) sum[0][0] += red[(k2 * S::kFrags + f) * kWave + lane];
+            if constexpr (kSplitK) {
+                // Across workgroups, the fragment is the unit: its last split sums and stores it.
+                if (!join_split<S::kFrags, 1, 1>(p, sum, tile_id, split, f, lane)) continue;
+            }
             if (p.col_scale) {
                 store_tiles<1, 1, kOutBf16>(p, sum, m0 + 16 * i, col0, lane, col_scales, bias_bits);
             } else {
@@ -935,6 +952,9 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             }
         }
     } else {
+        if constexpr (kSplitK) {
+            if (!join_split<WN, RM, RN>(p, acc, tile_id, split, wave_n, lane)) return;
+        }
         store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0, n0, lane, scale);
     }
 }

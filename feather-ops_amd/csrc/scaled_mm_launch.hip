@@ -36,11 +36,15 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
                                dim3(static_cast<uint32_t>(tiles)), dim3(S::kThreads), 0, stream, p);
         }
     } else {
-        if (p.splits != 1) return false;  // the streaming kernel splits K inside its workgroups only
         using S = StreamShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
-        hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16>), dim3(static_cast<uint32_t>(tiles)),
-                           dim3(S::kThreads), 0, stream, p);
+        if (p.splits > 1) {
+            hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true>),
+                               dim3(static_cast<uint32_t>(tiles * p.splits)), dim3(S::kThreads), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false>),
+                               dim3(static_cast<uint32_t>(tiles)), dim3(S::kThreads), 0, stream, p);
+        }
     }
     return true;
 }

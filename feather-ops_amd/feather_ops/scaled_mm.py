@@ -31,6 +31,7 @@ _TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
 _TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
 _TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
 _TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
+_TILE_STREAM_16x64 = (8, 1, 4, 1, 4, 0)
 
 # MI355X: 256 compute units.
 _CUS = 256
@@ -47,6 +48,13 @@ _RING_MODEL = (
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
 _SPLIT_MIN_K = 4096
 _SPLIT_MIN_STAGES = 16
+# The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (from
+# about 200 on, each CU's block already streams enough), aiming at _STREAM_SPLIT_BLOCKS workgroups with at
+# least _STREAM_SPLIT_MIN_RANGE of K each.
+_STREAM_SPLIT_MIN_K = 8192
+_STREAM_SPLIT_MAX_TILES = 192
+_STREAM_SPLIT_BLOCKS = 192
+_STREAM_SPLIT_MIN_RANGE = 2048
 
 
 def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
@@ -79,9 +87,11 @@ def select_scaled_mm_config(
     - M > 64 with a smaller grid and K >= 4096: the 128 x 128 ring tile (96 tiles or more) or the
       64 x 128 ring tile (48 or more 128 x 128 tiles), split along K (`select_scaled_mm_splits`).
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
-    - 16 < M <= 64: the 32-row streaming tile when it gives a CU's worth of blocks.
+    - 16 < M <= 32: the 32-row streaming tile when it gives a CU's worth of blocks.
+    - K >= 8192 with fewer than 192 16 x 64 streaming tiles: that tile (8 K slices per block), split along
+      K across workgroups (`select_scaled_mm_splits`).
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
-      columns), with 8 K slices per block unless there are 512 blocks or more, then 4.
+      columns), with 8 K slices per block up to one block per CU, 4 beyond (two blocks share a CU).
     """
     del a_dtype, b_dtype, out_dtype
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
@@ -93,26 +103,42 @@ def select_scaled_mm_config(
         return _TILE_RING_64x128
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
-    if 16 < M <= 64 and _blocks(M, N, _TILE_STREAM_32x64) >= _CUS:
+    if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) >= _CUS:
         return _TILE_STREAM_32x64
+    if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
+        return _TILE_STREAM_16x64
     rows = -(-M // 16)
     for repeat_n in (4, 2, 1):
         if rows * (N // (16 * repeat_n)) >= 160:
             break
     blocks = rows * -(-N // (16 * repeat_n))
-    return (8 if blocks < 2 * _CUS else 4, 1, 4, 1, repeat_n, 0)
+    return (8 if blocks <= _CUS else 4, 1, 4, 1, repeat_n, 0)
 
 
 def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> int:
     """K splits for a tile `select_scaled_mm_config` picked (1: none). Not in the reference, whose kernel
     has no split-K.
 
-    The split regime of `select_scaled_mm_config` (M > 64, K >= 4096, fewer 128 x 128 tiles than CUs)
-    splits its 128 x 128 or 64 x 128 ring tile into enough K ranges for about 512 workgroups (two per CU),
-    2 to 8 of them, each at least 16 stages of 64 deep. Measured 5-40% faster than the best unsplit tile
-    on the grid's cells in that regime; shorter K loses (the per-split fixed costs dominate).
+    Two split regimes of `select_scaled_mm_config`:
+    - M > 64, K >= 4096, fewer 128 x 128 tiles than CUs: its 128 x 128 or 64 x 128 ring tile splits into
+      enough K ranges for about 512 workgroups (two per CU), 2 to 8 of them, each at least 16 stages of
+      64 deep. Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
+    - K >= 8192 with fewer than 192 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
+      projection): that tile splits into about 192 workgroups (at most 128 tiles; 2 to 8 splits, each at
+      least 2048 deep), or 3 ways from 129 tiles on, so the blocks come close to whole multiples of the
+      CU count. Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
+      twelve such cells, within 4% of the best split count on most; at 224 tiles (16 x 14336 x 16384) the
+      unsplit tile is faster.
+    Shorter K loses: the per-split fixed costs (pipeline fill, the partial sums' round trip through
+    memory, the workspace lookup on the host) dominate.
     """
     tile = tuple(tile)
+    if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
+        tiles = _blocks(M, N, tile)
+        if tile != select_scaled_mm_config(M, N, K) or tiles >= _STREAM_SPLIT_MAX_TILES:
+            return 1
+        aim = round(_STREAM_SPLIT_BLOCKS / tiles) if tiles <= _CUS // 2 else 3
+        return max(2, min(8, aim, K // _STREAM_SPLIT_MIN_RANGE))
     if M <= 64 or K < _SPLIT_MIN_K or tile not in (_TILE_RING_128x128, _TILE_RING_64x128):
         return 1
     if tile != select_scaled_mm_config(M, N, K):
@@ -141,12 +167,18 @@ def _auto_choice(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int,
 _split_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
+# The workspace size per (M, N, K, tile, splits): the formula costs ~2 us of Python per call, the cache 0.2.
+_workspace_bytes = functools.lru_cache(maxsize=4096)(split_workspace_bytes)
+
+
 def _split_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    stream = torch.cuda.current_stream(device)
     if torch.cuda.is_current_stream_capturing():
         # Under graph capture the zero fill is recorded with the launch, so every replay starts clean.
         return torch.zeros(nbytes, dtype=torch.uint8, device=device)
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    # The raw handle of the current stream (what torch.cuda.current_stream(device).cuda_stream returns,
+    # without building a Stream object: a few microseconds less per launch).
+    key = (index, torch._C._cuda_getCurrentRawStream(index))
     ws = _split_workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -178,12 +210,12 @@ def _launch(
     if a.shape[0] == 0:  # an empty batch: the op checks its arguments and launches nothing
         ws = torch.empty(0, dtype=torch.uint8, device=a.device)
     else:
-        nbytes = split_workspace_bytes(a.shape[0], b_prepacked.shape[1], a.shape[1], tile, splits)
+        nbytes = _workspace_bytes(a.shape[0], b_prepacked.shape[1], a.shape[1], tuple(tile), splits)
         if nbytes < 0:
             raise RuntimeError(
-                f"split-K needs a ring tile and 1 <= splits <= the K stage count, got {tile}, {splits}")
+                f"split-K needs an instantiated tile and 1 <= splits <= the K units, got {tile}, {splits}")
         ws = _split_workspace(a.device, nbytes)
-    torch.ops.feather_ops.scaled_mm_splitk.default(a, b_prepacked, scale, bias, out, ws, splits, *tile[:5])
+    torch.ops.feather_ops.scaled_mm_splitk.default(a, b_prepacked, scale, bias, out, ws, splits, *tile)
 
 
 @custom_op("feather_ops::scaled_mm_auto", mutates_args=("out",))
@@ -210,8 +242,8 @@ def scaled_mm_hip(
     """`(a @ b^T) * scale + bias` against the prepacked fp8 weight `b_prepacked`.
 
     `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it. `splits` (not in the
-    reference) pins the split-K count of a ring tile; by default the heuristic picks it when `tile` is
-    None and a pinned tile runs unsplit.
+    reference) pins the split-K count; by default the heuristic picks it when `tile` is None and a pinned
+    tile runs unsplit.
     """
     _lib.require_native()
     out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)

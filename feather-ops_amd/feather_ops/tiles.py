@@ -17,14 +17,15 @@ Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, rep
   activation ring has 2 slots for blocks of up to 4 waves (so two or three blocks share a CU) and 3 for
   8-wave blocks, and the weight ring one more when it fits (see `ring_slots`), so the next stages are in
   flight while the current one feeds the MFMAs.
-- A ring tile can also split K across workgroups (`scaled_mm_hip(..., splits=S)`, the C ABI's
-  `feather_scaled_mm_splitk`): each output tile's stages are cut into S contiguous ranges whose fp32
-  partial sums meet in a caller-owned workspace (`split_workspace_bytes`), for grids with fewer tiles
-  than the GPU has compute units.
 - `prefetch = 0` selects the streaming kernel for skinny M: no LDS staging. The block's `warps_m` waves
   split K instead of M (so `block_m = 16 * repeat_m`), its `warps_n` waves split N, and each wave streams
   its operands from HBM into registers `chunk_k` at a time, double-buffered; a short LDS reduction joins
   the K slices in a fixed order.
+- Either kernel can also split K across workgroups (`scaled_mm_hip(..., splits=S)`, the C ABI's
+  `feather_scaled_mm_splitk`): each output tile's K range (a ring tile's `chunk_k`-deep stages, a
+  streaming tile's 64-deep groups) is cut into S contiguous ranges whose fp32 partial sums meet in a
+  caller-owned workspace (`split_workspace_bytes`), for grids with fewer tiles than the GPU has compute
+  units.
 """
 
 SCALED_MM_TILES = [
@@ -84,27 +85,40 @@ MAX_SPLITS = 32
 SPLIT_COUNTER_BYTES = 64 * 1024  # fixed counter area at the start of every split workspace
 
 
+def split_units(K: int, tile: tuple[int, ...]) -> int:
+    """The units a split launch cuts K into: a ring tile's `chunk_k`-deep stages, a streaming tile's 64-deep
+    groups."""
+    return -(-K // (16 * tile[2])) if tile[5] else -(-K // 64)
+
+
+def split_slots(tile: tuple[int, ...]) -> int:
+    """Join slots (arrival counters) per output tile of a split launch: a ring tile's waves, a streaming
+    tile's 16 x 16 fragments (its column waves when the block has a single K slice)."""
+    warps_m, warps_n, _, repeat_m, repeat_n, prefetch = tile[:6]
+    if prefetch:
+        return warps_m * warps_n
+    return warps_n * repeat_m * repeat_n if warps_m > 1 else warps_n
+
+
 def split_workspace_bytes(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> int:
     """Workspace bytes of a split-K launch (the C ABI's `feather_splitk_workspace_bytes`), -1 if the tile is
-    not a ring tile, `splits` is outside 1 .. min(32, K's stage count) or the grid has more than 16384
-    (tile, wave) pairs.
+    not instantiated, `splits` is outside 1 .. min(32, `split_units`) or the grid needs more than 16384
+    join counters (output tiles x `split_slots`).
 
-    Layout (none for `splits` = 1): a fixed 64 KiB counter area (one uint32 arrival counter per output tile and wave; it is the
-    same area for every shape, so a workspace reused across shapes keeps it zero), then `splits` fp32
-    partial tiles per output tile.
+    Layout (none for `splits` = 1): a fixed 64 KiB counter area (one uint32 arrival counter per output tile
+    and join slot; it is the same area for every shape, so a workspace reused across shapes keeps it
+    zero), then `splits` fp32 partial tiles per output tile.
     """
     tile = tuple(tile)
-    if M < 1 or N < 1 or K < 16 or len(tile) < 6 or tile[5] != 1 or tile not in SCALED_MM_TILES:
+    if M < 1 or N < 1 or K < 16 or len(tile) < 6 or tile not in SCALED_MM_TILES:
         return -1
-    warps_m, warps_n, unroll_k, _, _ = tile[:5]
-    stages = -(-K // (16 * unroll_k))
-    if not 1 <= splits <= min(MAX_SPLITS, stages):
+    if not 1 <= splits <= min(MAX_SPLITS, split_units(K, tile)):
         return -1
     if splits == 1:
         return 0
     block_m, block_n, _ = gemm_block_sizes(tile)
     tiles = -(-M // block_m) * -(-N // block_n)
-    if tiles * warps_m * warps_n * 4 > SPLIT_COUNTER_BYTES:
+    if tiles * split_slots(tile) * 4 > SPLIT_COUNTER_BYTES:
         return -1
     total = SPLIT_COUNTER_BYTES + tiles * splits * block_m * block_n * 4
     return total if total < 2**31 else -1

@@ -49,8 +49,8 @@ bool launch_scaled_mm(const uint16_t* a, const uint8_t* b_prepacked, const float
 
 /*
  * Split-K form of launch_scaled_mm for grids with fewer output tiles than the GPU has compute units: the
- * same arguments and contract, a ring-kernel tile (prefetch = 1 in the tile table), and each tile's K range
- * cut into `splits` contiguous ranges computed by separate workgroups. The partial sums (fp32) meet in
+ * same arguments and contract (any instantiated tile, ring or streaming), and each tile's K range cut into
+ * `splits` contiguous ranges computed by separate workgroups. The partial sums (fp32) meet in
  * `workspace`; the last workgroup of a tile to finish adds them in split order and stores the tile, so
  * results are deterministic and differ from the unsplit launch only by fp32 summation order.
  *
@@ -61,21 +61,23 @@ bool launch_scaled_mm(const uint16_t* a, const uint8_t* b_prepacked, const float
  *     them zero again, whatever its shape, so zero the workspace once, not per call;
  *   - calls that share a workspace must be ordered (one stream); concurrent calls need their own.
  * splits = 1 runs the unsplit kernel and ignores the workspace. Returns false (nothing enqueued) for a
- * contract violation, a streaming tile, splits outside 1 .. min(32, ceil(K / (16 * unroll_k))), a grid of
- * more than 16384 (tile, wave) pairs, or a missing or short workspace.
+ * contract violation, a tile that is not instantiated, splits outside 1 .. min(32, units of K) (a ring
+ * tile's units are its ceil(K / (16 * unroll_k)) stages, a streaming tile's the ceil(K / 64) groups), more
+ * than 16384 join counters (tiles x slots: a ring tile's waves, a streaming tile's 16 x 16 fragments), or
+ * a missing or short workspace.
  */
 bool feather_scaled_mm_splitk(const uint16_t* a, const uint8_t* b_prepacked, const float* scale,
                               const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K, int has_scale,
                               int has_bias, bool use_fp8_e5m2, bool a_bf16, bool output_bf16, int block_warps_m,
-                              int block_warps_n, int unroll_k, int repeat_m, int repeat_n, int splits,
-                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+                              int block_warps_n, int unroll_k, int repeat_m, int repeat_n, bool prefetch,
+                              int splits, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * Workspace bytes feather_scaled_mm_splitk needs for this shape, tile and split count (host only, no GPU
  * call): 0 for splits = 1, -1 if they are outside its contract. Always under 2 GiB.
  */
 int64_t feather_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int block_warps_m, int block_warps_n,
-                                       int unroll_k, int repeat_m, int repeat_n, int splits);
+                                       int unroll_k, int repeat_m, int repeat_n, bool prefetch, int splits);
 
 /*
  * out[i] = bf16 -> fp16 of in[i] with round-toward-zero (finite overflow saturates to +-65504, inf/NaN

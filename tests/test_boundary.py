@@ -36,10 +36,11 @@ def lib():
                                          ctypes.c_void_p]
     handle.feather_scaled_mm_splitk.restype = ctypes.c_bool
     handle.feather_scaled_mm_splitk.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + \
-        [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 6 + [ctypes.c_void_p, ctypes.c_int64,
-                                                                           ctypes.c_void_p]
+        [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_int] + \
+        [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     handle.feather_splitk_workspace_bytes.restype = ctypes.c_int64
-    handle.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 6
+    handle.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 5 + \
+        [ctypes.c_bool, ctypes.c_int]
     return handle
 
 
@@ -84,16 +85,18 @@ def test_c_abi_refuses_out_of_contract_calls(lib, kwargs):
 WS = 0x100000  # fake, 256-byte aligned workspace address
 
 
-def _split(lib, tile=(2, 2, 4, 4, 4), splits=2, ws=WS, ws_bytes=1 << 30, M=64, N=128, K=256, c=C):
+def _split(lib, tile=(2, 2, 4, 4, 4, True), splits=2, ws=WS, ws_bytes=1 << 30, M=64, N=128, K=256, c=C):
     return lib.feather_scaled_mm_splitk(A, B, S, BIAS, c, M, N, K, 1, 1, True, False, False, *tile, splits, ws,
                                         ws_bytes, None)
 
 
 @pytest.mark.parametrize("kwargs", [
-    dict(tile=(4, 1, 4, 1, 4)),            # a streaming tile: only the ring kernel splits K
-    dict(tile=(3, 3, 3, 3, 3)),            # not instantiated
+    dict(tile=(4, 1, 4, 1, 4, True)),      # right numbers, wrong kernel family: not instantiated
+    dict(tile=(3, 3, 3, 3, 3, True)),      # not instantiated
     dict(splits=0),
     dict(splits=5),                        # K = 256 has 4 stages of 64
+    dict(splits=5, tile=(4, 1, 8, 1, 4, False)),  # a streaming tile splits K = 256's 4 groups of 64
+    dict(splits=33, K=4096, tile=(8, 1, 4, 1, 4, False)),
     dict(splits=33, K=4096),               # above the 32 maximum
     dict(ws=None),
     dict(ws=WS + 16),                      # workspace not 256-byte aligned
@@ -110,15 +113,23 @@ def test_splitk_workspace_bytes_match_the_python_formula(lib):
     for tile in SCALED_MM_TILES:
         for m, n, k in [(1, 8, 16), (67, 272, 304), (512, 5376, 5120), (4096, 3072, 3072)]:
             for splits in (0, 1, 2, 3, 8, 32, 33):
-                want = lib.feather_splitk_workspace_bytes(m, n, k, *tile[:5], splits) if tile[5] else -1
+                want = lib.feather_splitk_workspace_bytes(m, n, k, *tile, splits)
                 assert split_workspace_bytes(m, n, k, tile, splits) == want, (tile, m, n, k, splits)
+    ws = lib.feather_splitk_workspace_bytes
     # 512 x 5376 with 128 x 128 tiles: the 64 KiB counter area, then 168 tiles x 3 fp32 partial tiles
-    assert lib.feather_splitk_workspace_bytes(512, 5376, 5120, 2, 2, 4, 4, 4, 3) == 65536 + 168 * 3 * 128 * 128 * 4
+    assert ws(512, 5376, 5120, 2, 2, 4, 4, 4, True, 3) == 65536 + 168 * 3 * 128 * 128 * 4
     # 16384 (tile, wave) counters at most: 4096 128 x 128 tiles of 4 waves fit, 4097 do not
-    assert lib.feather_splitk_workspace_bytes(4096, 16384, 256, 2, 2, 4, 4, 4, 2) > 0
-    assert lib.feather_splitk_workspace_bytes(4096, 16392, 256, 2, 2, 4, 4, 4, 2) == -1
-    assert lib.feather_splitk_workspace_bytes(4096, 16392, 256, 2, 2, 4, 4, 4, 1) == 0  # unsplit: no workspace
-    assert lib.feather_splitk_workspace_bytes(512, 5376, 5120, 4, 1, 4, 1, 4, 2) == -1  # streaming tile
+    assert ws(4096, 16384, 256, 2, 2, 4, 4, 4, True, 2) > 0
+    assert ws(4096, 16392, 256, 2, 2, 4, 4, 4, True, 2) == -1
+    assert ws(4096, 16392, 256, 2, 2, 4, 4, 4, True, 1) == 0  # unsplit: no workspace
+    # a 16 x 64 streaming tile: 84 x 2 tiles of 4 fragments, 16 x 64 fp32 partials per split
+    assert ws(32, 5376, 5120, 8, 1, 4, 1, 4, False, 4) == 65536 + 168 * 4 * 16 * 64 * 4
+    # streaming splits count 64-deep groups whatever unroll_k is: K = 256 has 4
+    assert ws(16, 64, 256, 8, 1, 8, 1, 4, False, 4) > 0 and ws(16, 64, 256, 8, 1, 8, 1, 4, False, 5) == -1
+    # 16384 (tile, fragment) counters: 4096 tiles of 4 fragments fit, 4097 do not
+    assert ws(16, 4096 * 64, 256, 8, 1, 4, 1, 4, False, 2) > 0
+    assert ws(16, 4096 * 64 + 64, 256, 8, 1, 4, 1, 4, False, 2) == -1
+    assert ws(512, 5376, 5120, 4, 1, 4, 1, 4, True, 2) == -1  # no such ring tile
 
 
 def test_convert_c_abi_refuses_bad_arguments(lib):
@@ -170,7 +181,7 @@ def test_torch_ops_are_registered_for_the_gpu_only():
                                                 torch.empty(8, 8, 16, dtype=torch.float8_e5m2))
     with pytest.raises((NotImplementedError, RuntimeError)):
         torch.ops.feather_ops.scaled_mm_splitk.default(a, b, None, None, c, torch.zeros(1 << 16, dtype=torch.uint8),
-                                                       2, 2, 2, 4, 4, 4)
+                                                       2, 2, 2, 4, 4, 4, True)
 
 
 def test_scaled_mm_hip_has_no_cpu_fallback():
@@ -197,11 +208,23 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(1040, 1024, 5120) == ((1, 4, 4, 4, 2, 1), 3)    # 72 tiles of 128 x 128: 64 x 128, 136 tiles
     assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
     assert auto(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)    # short K: no split
-    assert auto(192, 1536, 6144) == ((8, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
+    assert auto(192, 1536, 6144) == ((4, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
     assert auto(4096, 12288, 3072) == ((2, 2, 4, 4, 8, 1), 1)   # full grids never split
     assert auto(16, 14336, 4096)[1] == 1
+    # skinny M, long K, fewer than 192 16 x 64 streaming tiles: that tile, split for about 192 workgroups
+    assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 4, 0), 3)      # 64 tiles
+    assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 4, 0), 3)
+    assert auto(1, 8192, 28672) == ((8, 1, 4, 1, 4, 0), 2)      # 128 tiles -> 256 workgroups
+    assert auto(32, 5120, 25600) == ((8, 1, 4, 1, 4, 0), 3)     # 160 tiles (2 row blocks): 3 from 129 on
+    assert auto(16, 2048, 8192) == ((8, 1, 4, 1, 4, 0), 4)      # 32 tiles, but K ranges of 2048 at least
+    assert auto(1, 512, 65536) == ((8, 1, 4, 1, 4, 0), 8)       # at most 8
+    assert auto(16, 14336, 16384) == ((8, 1, 4, 1, 4, 0), 1)    # 224 tiles: unsplit
+    assert auto(8, 28672, 8192) == ((4, 1, 4, 1, 4, 0), 1)      # 448 tiles: a full grid, 4 slices, unsplit
+    assert auto(16, 4096, 6144) == ((8, 1, 4, 1, 1, 0), 1)      # K < 8192: narrower tiles instead
+    assert auto(32, 25600, 8192) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
+    assert splits(16, 14336, 16384, (8, 1, 4, 1, 4, 0)) == 1    # 224 tiles
     for m in (65, 128, 200, 512, 1040, 2320):
         for n in (1024, 1536, 4096, 12288):
             for k in (4096, 6144, 16384):

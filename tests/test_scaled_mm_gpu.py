@@ -129,11 +129,13 @@ def test_heuristic_matches_a_measured_tile(fo):
     check_against_oracle(out, a, bp, scale, None, rows=sample_rows(4112))
 
 
-# One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, the
-# 32-row streaming tile, the 64 x 64 ring tile for mid-size grids, and the wave-quantization choice among
-# 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out with a bias, against the oracle.
+# One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, split
+# across workgroups for long K, the 32-row streaming tile, the 64 x 64 ring tile for mid-size grids, and the
+# wave-quantization choice among 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out
+# with a bias, against the oracle.
 HEURISTIC_CELLS = [
-    (2, 4096, 16384),    # 16 x 16 columns, 8 slices
+    (2, 4096, 16384),    # 16 x 64 streaming tile split 3 ways along K across workgroups
+    (16, 4096, 4096),    # 16 x 16 columns, 8 slices
     (16, 6144, 6144),    # 16 x 32 columns
     (32, 25600, 5120),   # 32-row streaming tile
     (128, 1024, 5120),   # 16-row tile, 8 row blocks

@@ -2,10 +2,11 @@
 `feather_scaled_mm_splitk`) against the CPU oracle.
 
 Split-K changes only the fp32 summation order, so every case meets the same bar as the unsplit kernel
-(`check_against_oracle`). Also checked: every ring tile with ragged M, N and K; split counts up to the
-stage count; bias, per-column scales, bf16 activations (the register-staged path), e4m3fn, both output
-dtypes; determinism; a shared workspace reused with alternating inputs (no stale partial sums are read);
-the workspace counters back at zero after each call; graph replay; the C ABI called directly; and the
+(`check_against_oracle`). Also checked: every ring tile and every streaming tile with ragged M, N and K;
+split counts up to the stage (ring) or 64-deep group (streaming) count; bias, per-column scales, bf16
+activations (the register-staged path), e4m3fn, both output dtypes; determinism; a shared workspace
+reused with alternating inputs and across kernel families (no stale partial sums are read); the
+workspace counters back at zero after each call; graph replay; the C ABI called directly; and the
 refusals of the op.
 """
 
@@ -40,6 +41,12 @@ def _ring_tiles():
     return [t for t in SCALED_MM_TILES if t[5] == 1]
 
 
+def _stream_tiles():
+    from feather_ops.tiles import SCALED_MM_TILES
+
+    return [t for t in SCALED_MM_TILES if t[5] == 0]
+
+
 def _stages(k, tile):
     return -(-k // (16 * tile[2]))
 
@@ -55,6 +62,80 @@ def test_every_ring_tile_split(fo, tile, splits):
     bias = _tensor((N,), torch.bfloat16, seed=2)
     out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile, splits=splits)
     check_against_oracle(out, a, bp, scale, bias)
+
+
+@pytest.mark.parametrize("tile", _stream_tiles())
+@pytest.mark.parametrize("splits", [2, 3, 7])
+def test_every_stream_tile_split(fo, tile, splits):
+    """Ragged M (not a multiple of the 16-row fragment), N (N % 16 == 8) and K: K = 1040 is 17 groups of 64,
+    the last one a single chunk of 16, so a split can hold fewer groups than the block has K slices."""
+    M, N, K = 37, 264, 1040
+    a = _tensor((M, K), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    scale = torch.tensor(0.75, device="cuda")
+    bias = _tensor((N,), torch.bfloat16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile, splits=splits)
+    check_against_oracle(out, a, bp, scale, bias)
+
+
+@pytest.mark.parametrize("a_dtype,b_dtype,out_dtype", [(torch.bfloat16, torch.float8_e4m3fn, torch.float16),
+                                                       (torch.float16, torch.float8_e5m2, torch.bfloat16)])
+def test_stream_split_dtypes_with_column_scales(fo, a_dtype, b_dtype, out_dtype):
+    M, N, K = 5, 1032, 2048
+    a = _tensor((M, K), a_dtype)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), b_dtype, seed=1))
+    scale = (torch.rand(N, generator=torch.Generator().manual_seed(3)) + 0.5).cuda()
+    bias = _tensor((N,), out_dtype, seed=2)
+    for tile in [(8, 1, 4, 1, 4, 0), (4, 2, 4, 1, 2, 0), (2, 2, 4, 4, 2, 0)]:
+        out = fo.scaled_mm_hip(a, bp, scale, bias, out_dtype, tile=tile, splits=4)
+        check_against_oracle(out, a, bp, scale, bias)
+
+
+@pytest.mark.parametrize("m,n,k,tile,splits", [
+    (16, 14336, 4096, (8, 1, 4, 1, 4, 0), 2),     # the weight-streaming cell
+    (32, 5120, 25600, (2, 2, 4, 2, 2, 0), 4),
+    (2, 4096, 16384, (8, 1, 4, 1, 4, 0), 4),
+    (1, 3072, 3072, (8, 1, 4, 1, 2, 0), 3),
+])
+def test_stream_split_full_size(fo, m, n, k, tile, splits):
+    a = _tensor((m, k), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
+    scale = torch.tensor(0.02, device="cuda")
+    bias = _tensor((n,), torch.float16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, torch.float16, tile=tile, splits=splits)
+    check_against_oracle(out, a, bp, scale, bias, rows=sample_rows(m))
+
+
+def test_stream_split_count_up_to_the_group_count(fo):
+    M, N, K = 16, 128, 1024  # 16 groups of 64, whatever the tile's unroll_k
+    a = _tensor((M, K), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
+    tile = (8, 1, 8, 1, 4, 0)
+    unsplit = fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile)
+    for splits in (2, 16):
+        out = fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile, splits=splits)
+        check_against_oracle(out, a, bp, None, None)
+        assert (out.float() - unsplit.float()).abs().max().item() <= unsplit.float().abs().max().item() * 2**-9
+    with pytest.raises(RuntimeError):
+        fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile, splits=17)
+
+
+def test_workspace_reuse_across_kernel_families(fo):
+    """Ring and streaming split launches alternate on one workspace; the streaming counters (one per
+    fragment) and the ring ones (one per wave) share the fixed area, and every call leaves it zero."""
+    from feather_ops.scaled_mm import _split_workspaces
+
+    cases = [(16, 5376, 4096, (8, 1, 4, 1, 4, 0), 3), (300, 1000, 2048, (2, 2, 4, 4, 4, 1), 4),
+             (3, 2056, 1600, (4, 2, 4, 1, 2, 0), 5), (64, 640, 4096, (2, 2, 4, 4, 2, 0), 8),
+             (16, 5376, 4096, (8, 1, 4, 1, 4, 0), 3)]
+    for i, (m, n, k, tile, splits) in enumerate(cases):
+        a = _tensor((m, k), torch.float16, seed=60 + i)
+        bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=70 + i))
+        out = fo.scaled_mm_hip(a, bp, None, None, torch.float16, tile=tile, splits=splits)
+        check_against_oracle(out, a, bp, None, None, rows=sample_rows(m))
+    torch.cuda.synchronize()
+    ws = _split_workspaces[(torch.cuda.current_device(), torch.cuda.current_stream().cuda_stream)]
+    assert int(ws[: 64 * 1024].view(torch.int32).abs().sum().item()) == 0
 
 
 @pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
@@ -224,16 +305,18 @@ def test_c_abi_direct(fo):
     lib = ctypes.CDLL(str(_lib.LIBRARY))
     lib.feather_scaled_mm_splitk.restype = ctypes.c_bool
     lib.feather_scaled_mm_splitk.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + \
-        [ctypes.c_bool] * 3 + [ctypes.c_int] * 6 + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_int] + \
+        [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     lib.feather_splitk_workspace_bytes.restype = ctypes.c_int64
-    lib.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 6
+    lib.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 5 + \
+        [ctypes.c_bool, ctypes.c_int]
     M, N, K = 100, 256, 640
     a = _tensor((M, K), torch.bfloat16)
     bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e5m2, seed=1))
     s = torch.tensor(0.3, device="cuda")
     bias = _tensor((N,), torch.float16, seed=2)
-    tile = (2, 2, 4, 4, 4)
-    want = fo.scaled_mm_hip(a, bp, s, bias, torch.float16, tile=tile + (1,), splits=5)
+    tile = (2, 2, 4, 4, 4, True)
+    want = fo.scaled_mm_hip(a, bp, s, bias, torch.float16, tile=tile, splits=5)
     need = lib.feather_splitk_workspace_bytes(M, N, K, *tile, 5)
     ws = torch.zeros(need + 256, dtype=torch.uint8, device="cuda")
     c = torch.empty_like(want)
@@ -258,7 +341,7 @@ def test_op_rejects_bad_split_arguments(fo):
     ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
     op = torch.ops.feather_ops.scaled_mm_splitk.default
     with pytest.raises(RuntimeError, match="Unsupported config"):
-        op(a, bp, None, None, c, ws, 2, 4, 1, 4, 1, 4)          # streaming tile
+        op(a, bp, None, None, c, ws, 2, 4, 1, 4, 1, 4)          # a streaming tile's numbers as a ring tile
     with pytest.raises(RuntimeError, match="workspace must hold"):
         op(a, bp, None, None, c, ws[:1024], 2, 2, 2, 4, 4, 4)
     with pytest.raises(RuntimeError, match="256-byte aligned"):

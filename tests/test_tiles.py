@@ -78,7 +78,7 @@ def _check_lds():
 
 def test_every_kernel_allocates_exactly_its_tiles_lds():
     """The LDS audit (check_lds.py, the reference's tools/check_lds.py role): the compiled gfx950 code
-    object's group_segment_fixed_size of every ring (unsplit and split) and streaming instantiation equals
+    object's group_segment_fixed_size of every ring and streaming instantiation (unsplit and split) equals
     the size the tile asks for. Compiles one dtype combination (hipcc, device code only)."""
     import pytest
 
@@ -89,9 +89,7 @@ def test_every_kernel_allocates_exactly_its_tiles_lds():
         pytest.skip("needs hipcc")
     asm = check.compile_asm("100")
     checked, bad = check.audit(asm)
-    ring = sum(1 for t in SCALED_MM_TILES if t[5] == 1)
-    stream = len(SCALED_MM_TILES) - ring
-    assert checked == 2 * ring + stream
+    assert checked == 2 * len(SCALED_MM_TILES)
     assert bad == []
     # a planted off-by-one in the expectation is caught for every instantiation
     real = check.expected_bytes
