@@ -159,33 +159,43 @@ def time_c2(steps: int = 100, warmup: int = 10):
     return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
 
 
-def time_splitk(steps: int = 100, warmup: int = 10):
-    """A split-K cell (fp16 [512, 5120] x e5m2 [5376, 5120] -> fp16: 168 tiles of 128 x 128 for 256 CUs),
-    TFLOP/s of the heuristic's pick (split along K) and of the best unsplit tile, timed the same way."""
+def time_split_cell(m: int, k: int, n: int, unsplit_tile, copies: int = 1, steps: int = 100, warmup: int = 10):
+    """A split-K cell: the heuristic's pick (split along K) and an unsplit tile on fp16 [m, k] x e5m2 [n, k]
+    -> fp16, each launched back to back through the op with one preallocated workspace (so the Python
+    layer's per-call cost is not timed), rotating over `copies` weights. Returns us, TFLOP/s and GB/s of
+    algorithmic bytes for both."""
     import torch
 
     import feather_ops
-    from feather_ops.scaled_mm import _launch, select_scaled_mm_splits
+    from feather_ops.scaled_mm import select_scaled_mm_splits
+    from feather_ops.tiles import split_workspace_bytes
 
-    m, k, n = 512, 5120, 5376
-    a, bs, s = make_device_inputs(m, k, n, "fp16")
-    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    a, bs, s = make_device_inputs(m, k, n, "fp16", copies=copies)
+    tile = tuple(feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16))
     splits = select_scaled_mm_splits(m, n, k, tile)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
-    res = {"tile": list(tile), "splits": splits}
-    for name, t, sp in (("auto", tile, splits), ("unsplit", (2, 2, 4, 2, 2, 1), 1)):
-        for _ in range(warmup):
-            _launch(a, bs[0], s, None, out, t, sp)
+    ws = torch.zeros(max(split_workspace_bytes(m, n, k, tile, splits), 1), dtype=torch.uint8, device="cuda")
+    nbytes = 2 * m * k + -(-k // 128) * 128 * n + 2 * m * n + 4
+    res = {"tile": list(tile), "splits": splits, "unsplit_tile": list(unsplit_tile)}
+    for name, t, sp in (("auto", tile, splits), ("unsplit", tuple(unsplit_tile), 1)):
+        def launch(i, t=t, sp=sp):
+            if sp == 1:
+                torch.ops.feather_ops.scaled_mm.default(a, bs[i % copies], s, None, out, *t)
+            else:
+                torch.ops.feather_ops.scaled_mm_splitk.default(a, bs[i % copies], s, None, out, ws, sp, *t)
+        for i in range(warmup):
+            launch(i)
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for _ in range(steps):
-            _launch(a, bs[0], s, None, out, t, sp)
+        for i in range(steps):
+            launch(i)
         stop.record(stream)
         torch.cuda.synchronize()
         ms = start.elapsed_time(stop) / steps
-        res[name] = {"us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+        res[name] = {"us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+                     "gbps": nbytes / (ms * 1e-3) / 1e9}
     return res
 
 
@@ -257,7 +267,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    parser.add_argument("--no-secondary", action="store_true", help="skip the C4 (HBM), C2 (bf16) and split-K cells")
+    parser.add_argument("--no-secondary", action="store_true",
+                        help="skip the C4 (HBM), C2 (bf16) and split-K cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()
@@ -279,7 +290,11 @@ def main() -> int:
     c3 = time_c3(args.steps, args.warmup)
     c4 = None if args.no_secondary else time_c4()
     c2 = None if args.no_secondary else time_c2()
-    sk = None if args.no_secondary else time_splitk()
+    # 168 tiles of 128 x 128 for 256 CUs; the unsplit control is the best unsplit tile of the sweep
+    sk = None if args.no_secondary else time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1))
+    # a decoder's down projection at batch 2: 64 tiles of 16 x 64, 67 MB of weight, 8 rotated copies; the
+    # unsplit control is the streaming tile the heuristic picks without split-K (16 x 16, 256 blocks)
+    dk = None if args.no_secondary else time_split_cell(2, 16384, 4096, (8, 1, 4, 1, 1, 0), copies=8)
     cpu = None if args.no_cpu else time_cpu_oracle()
 
     line = {
@@ -317,6 +332,14 @@ def main() -> int:
                                "tile": sk["tile"], "splits": sk["splits"],
                                "TFLOPs": round(sk["auto"]["tflops"], 1), "us_per_launch": round(sk["auto"]["us"], 2),
                                "unsplit_64x64_TFLOPs": round(sk["unsplit"]["tflops"], 1)}
+    if dk is not None:
+        line["decode_split_cell"] = {"workload": "skinny long K: fp16 [2,16384] x e5m2 [4096,16384] -> fp16, "
+                                                 "8 rotated weights",
+                                     "tile": dk["tile"], "splits": dk["splits"], "GBps": round(dk["auto"]["gbps"], 1),
+                                     "us_per_launch": round(dk["auto"]["us"], 2),
+                                     "frac_hbm_peak": round(dk["auto"]["gbps"] / PEAK_HBM_GBPS, 4),
+                                     "unsplit_tile": dk["unsplit_tile"],
+                                     "unsplit_GBps": round(dk["unsplit"]["gbps"], 1)}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))

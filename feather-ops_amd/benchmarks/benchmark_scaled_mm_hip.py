@@ -20,7 +20,8 @@ Run from `feather-ops_amd/`:
 
 `auto` is the whole heuristic (tile and split count). With `--splits`, every listed tile (ring or
 streaming) whose grid has fewer tiles than the GPU has compute units is also timed split `S` ways (named
-`(tile)/S`), for each `S` that keeps at most four workgroups per CU. Every provider calls its op directly
+`(tile)/S`), for each `S` that keeps at most four workgroups per CU (`--split-any-grid`: whatever the
+grid, under that same cap). Every provider calls its op directly
 (split launches with one preallocated workspace per cell), so the Python layer's per-call cost is not
 timed; `--graph` also takes the op dispatch out (replays of captured batches), which matters for kernels
 of a few microseconds.
@@ -97,7 +98,7 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, out_dtype))
     picked_splits = select_scaled_mm_splits(m, n, k, picked)
     split_cases = [(tile, splits) for tile in tiles for splits in args.splits
-                   if _blocks(m, n, tile) < _CUS and _blocks(m, n, tile) * splits <= 4 * _CUS
+                   if (_blocks(m, n, tile) < _CUS or args.split_any_grid) and _blocks(m, n, tile) * splits <= 4 * _CUS
                    and split_workspace_bytes(m, n, k, tile, splits) > 0]
     if picked_splits > 1:
         split_cases.append((picked, picked_splits))
@@ -143,6 +144,8 @@ def main() -> int:
     parser.add_argument("--square", action="store_true", help="N^3 for N in 512..8192 instead of the grid")
     parser.add_argument("--tiles", nargs="?", const="", default=None, help="'m,n,u,rm,rn,p;...', or nothing for all")
     parser.add_argument("--splits", default="", help="'2,3,4': split-K counts to time for underfilled grids")
+    parser.add_argument("--split-any-grid", action="store_true",
+                        help="time the split counts on grids of a CU's worth of tiles or more too")
     parser.add_argument("--a-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--out-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--no-bias", dest="bias", action="store_false")
@@ -178,6 +181,8 @@ def main() -> int:
               f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])}"
               f"{'/' + str(r['picked_splits']) if r['picked_splits'] > 1 else ''} -> {r['best']}",
               flush=True)
+        if args.json_path:  # after every cell, so a run cut short keeps what it measured
+            pathlib.Path(args.json_path).write_text(json.dumps({"args": vars(args), "results": results}, indent=1))
         torch.cuda.empty_cache()
     geo = lambda xs: math.exp(sum(math.log(x) for x in xs) / len(xs))  # noqa: E731
     print(f"geomean over {len(results)} cells: auto/best {geo([r['auto_vs_best'] for r in results]):.3f}, "

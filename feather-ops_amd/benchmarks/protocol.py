@@ -95,8 +95,7 @@ def _replay_ms(graph: torch.cuda.CUDAGraph, iters: int) -> float:
 def measure(providers: dict[str, Callable[[int], object]], *, warmup: int = 5, rounds: int = 5,
             target_ms: float = 20.0, max_iters: int = 64, graph: bool = False) -> dict[str, Measurement]:
     """Time each provider (called with a running launch index, which a provider may use to rotate its
-    weight copies) over `rounds` interleaved rounds; with `graph`, as replays of a captured batch of
-    `max_iters` launches."""
+    weight copies) over `rounds` interleaved rounds; with `graph`, as replays of a captured batch."""
     names = list(providers)
     for name in names:
         for i in range(warmup):
@@ -105,13 +104,11 @@ def measure(providers: dict[str, Callable[[int], object]], *, warmup: int = 5, r
     iters = {}
     graphs = {}
     for name in names:
+        one = max(_batch_ms(providers[name], 0, 1), 1e-4)
+        iters[name] = int(min(max(round(target_ms / one), 1), max_iters))
         if graph:
-            iters[name] = max_iters
-            graphs[name] = _capture(providers[name], max_iters)
-            _replay_ms(graphs[name], max_iters)  # warm replay
-        else:
-            one = max(_batch_ms(providers[name], 0, 1), 1e-4)
-            iters[name] = int(min(max(round(target_ms / one), 1), max_iters))
+            graphs[name] = _capture(providers[name], iters[name])
+            _replay_ms(graphs[name], iters[name])  # warm replay
     samples: dict[str, list[float]] = {name: [] for name in names}
     counter = 0
     for order in rotated_orders(names, rounds):

@@ -48,6 +48,11 @@ _RING_MODEL = (
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
 _SPLIT_MIN_K = 4096
 _SPLIT_MIN_STAGES = 16
+# 32 < M <= 64: the 64 x 128 ring tile from this many tiles on, split along K to about _MID_M_RING_BLOCKS
+# workgroups.
+_MID_M_RING_TILES = 128
+_MID_M_RING_BLOCKS = 512
+
 # The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (from
 # about 200 on, each CU's block already streams enough), aiming at _STREAM_SPLIT_BLOCKS workgroups with at
 # least _STREAM_SPLIT_MIN_RANGE of K each.
@@ -87,7 +92,10 @@ def select_scaled_mm_config(
     - M > 64 with a smaller grid and K >= 4096: the 128 x 128 ring tile (96 tiles or more) or the
       64 x 128 ring tile (48 or more 128 x 128 tiles), split along K (`select_scaled_mm_splits`).
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
-    - 16 < M <= 32: the 32-row streaming tile when it gives a CU's worth of blocks.
+    - 16 < M <= 64 with a wide N: the 64 x 128 ring tile, which reads the weight once where the 16-row
+      streaming tiles read it once per 16 rows: from 128 of its tiles when M > 32 (split along K to about
+      512 workgroups, `select_scaled_mm_splits`), from 512 when M <= 32.
+    - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
     - K >= 8192 with fewer than 192 16 x 64 streaming tiles: that tile (8 K slices per block), split along
       K across workgroups (`select_scaled_mm_splits`).
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
@@ -103,7 +111,11 @@ def select_scaled_mm_config(
         return _TILE_RING_64x128
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
-    if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) >= _CUS:
+    if 16 < M <= 64:
+        ring_tiles = _blocks(M, N, _TILE_RING_64x128)
+        if ring_tiles >= (_MID_M_RING_TILES if M > 32 else 2 * _CUS):
+            return _TILE_RING_64x128
+    if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) > 3 * _CUS // 2:
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
         return _TILE_STREAM_16x64
@@ -119,7 +131,7 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
     """K splits for a tile `select_scaled_mm_config` picked (1: none). Not in the reference, whose kernel
     has no split-K.
 
-    Two split regimes of `select_scaled_mm_config`:
+    Three split regimes of `select_scaled_mm_config`:
     - M > 64, K >= 4096, fewer 128 x 128 tiles than CUs: its 128 x 128 or 64 x 128 ring tile splits into
       enough K ranges for about 512 workgroups (two per CU), 2 to 8 of them, each at least 16 stages of
       64 deep. Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
@@ -129,10 +141,19 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
       CU count. Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
       twelve such cells, within 4% of the best split count on most; at 224 tiles (16 x 14336 x 16384) the
       unsplit tile is faster.
+    - 32 < M <= 64 on the 64 x 128 ring tile with fewer than 512 tiles: about 512 workgroups, up to 4
+      splits of at least 16 stages. At so few rows the ring is latency-bound (each block keeps only its
+      ring's few stages in flight), and more workgroups per CU keep more of the weight in flight:
+      64 x 16384 x 4096 377 TFLOP/s split 4 ways against 188 unsplit, 64 x 32768 x 4096 517 against 361.
     Shorter K loses: the per-split fixed costs (pipeline fill, the partial sums' round trip through
     memory, the workspace lookup on the host) dominate.
     """
     tile = tuple(tile)
+    if tile == _TILE_RING_64x128 and 32 < M <= 64:
+        if tile != select_scaled_mm_config(M, N, K):
+            return 1
+        aim = round(_MID_M_RING_BLOCKS / _blocks(M, N, tile))
+        return max(1, min(4, aim, -(-K // 64) // _SPLIT_MIN_STAGES))
     if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
         tiles = _blocks(M, N, tile)
         if tile != select_scaled_mm_config(M, N, K) or tiles >= _STREAM_SPLIT_MAX_TILES:

@@ -222,6 +222,15 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(8, 28672, 8192) == ((4, 1, 4, 1, 4, 0), 1)      # 448 tiles: a full grid, 4 slices, unsplit
     assert auto(16, 4096, 6144) == ((8, 1, 4, 1, 1, 0), 1)      # K < 8192: narrower tiles instead
     assert auto(32, 25600, 8192) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
+    # 16 < M <= 64 with a wide N: the 64 x 128 ring tile, split to about 512 workgroups when M > 32
+    assert auto(64, 16384, 4096) == ((1, 4, 4, 4, 2, 1), 4)     # 128 tiles
+    assert auto(48, 32768, 4096) == ((1, 4, 4, 4, 2, 1), 2)     # 256 tiles
+    assert auto(64, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # 512 tiles
+    assert auto(64, 16384, 1024) == ((1, 4, 4, 4, 2, 1), 1)     # 16 stages: too short to split
+    assert auto(64, 8192, 4096) == ((4, 1, 4, 1, 4, 0), 1)      # 64 tiles: streaming
+    assert auto(32, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # M <= 32: from 512 tiles
+    assert auto(32, 32768, 4096) == ((2, 2, 4, 2, 2, 0), 1)     # 512 32-row tiles
+    assert auto(32, 16384, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 256 32-row tiles: the 16-row tile
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
     assert splits(16, 14336, 16384, (8, 1, 4, 1, 4, 0)) == 1    # 224 tiles

@@ -130,7 +130,8 @@ def test_heuristic_matches_a_measured_tile(fo):
 
 
 # One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, split
-# across workgroups for long K, the 32-row streaming tile, the 64 x 64 ring tile for mid-size grids, and the
+# across workgroups for long K, the 32-row streaming tile, the 64 x 128 ring tile for 16 < M <= 64 with a
+# wide N, split or not, the 64 x 64 ring tile for mid-size grids, and the
 # wave-quantization choice among 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out
 # with a bias, against the oracle.
 HEURISTIC_CELLS = [
@@ -138,6 +139,8 @@ HEURISTIC_CELLS = [
     (16, 4096, 4096),    # 16 x 16 columns, 8 slices
     (16, 6144, 6144),    # 16 x 32 columns
     (32, 25600, 5120),   # 32-row streaming tile
+    (64, 16384, 4096),   # 64 x 128 ring tile at 64 rows, split 4 ways along K
+    (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
     (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
     (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways

@@ -64,6 +64,19 @@ def test_every_ring_tile_split(fo, tile, splits):
     check_against_oracle(out, a, bp, scale, bias)
 
 
+@pytest.mark.parametrize("m", [1, 20, 48, 64])
+def test_ring_split_with_fewer_rows_than_the_tile(fo, m):
+    """The 64 x 128 ring tile split along K at skinny M (the heuristic's 16 < M <= 64 regime): the rows
+    past M read as zeros and are never stored."""
+    N, K = 1032, 4096
+    a = _tensor((m, K), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), torch.float8_e4m3fn, seed=1))
+    scale = torch.tensor(0.5, device="cuda")
+    bias = _tensor((N,), torch.float16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, scale, bias, torch.float16, tile=(1, 4, 4, 4, 2, 1), splits=4)
+    check_against_oracle(out, a, bp, scale, bias)
+
+
 @pytest.mark.parametrize("tile", _stream_tiles())
 @pytest.mark.parametrize("splits", [2, 3, 7])
 def test_every_stream_tile_split(fo, tile, splits):
