@@ -2,7 +2,8 @@
 """Check every kernel instantiation's real LDS allocation against the size its tile asks for.
 
 The number the runtime allocates is the code object's `group_segment_fixed_size`; the kernels ask for a
-compile-time function of the tile (the ring kernel: its activation and weight rings, `tiles.ring_slots`;
+compile-time function of the tile (the ring kernel: its activation and weight rings, `tiles.ring_slots`,
+shallow or deep;
 the streaming kernel: per-wave activation double buffers plus the K-slice join). A mismatch costs
 occupancy, so it is a bug in the source or the compiler. Same role as the reference's
 `tools/check_lds.py:30-101`, for gfx950: it compiles `csrc/scaled_mm_launch.hip` for one dtype
@@ -31,11 +32,13 @@ def _tiles():
     return module
 
 
-def expected_bytes(kernel: str, ints: list[int]) -> int:
-    """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`)."""
+def expected_bytes(kernel: str, ints: list[int], bools: list[int] = ()) -> int:
+    """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`); a ring kernel's last template
+    flag is its deep-ring variant."""
     if kernel == "ring_dma_kernel":
         warps_m, warps_n, unroll_k, repeat_m, repeat_n = ints
-        slots_a, slots_b = _tiles().ring_slots((warps_m, warps_n, unroll_k, repeat_m, repeat_n, 1))
+        deep = bool(bools[-1]) if len(bools) == 5 else False
+        slots_a, slots_b = _tiles().ring_slots((warps_m, warps_n, unroll_k, repeat_m, repeat_n, 1), deep)
         a_stage = 16 * warps_m * repeat_m * unroll_k * 32
         b_stage = 16 * warps_n * repeat_n * unroll_k * 16
         return slots_a * a_stage + slots_b * b_stage
@@ -78,7 +81,7 @@ def audit(asm: str) -> tuple[int, list[tuple]]:
         ints = [int(v) for v in re.findall(r"Li(\d+)E", match.group(2))]
         bools = [int(v) for v in re.findall(r"Lb([01])E", match.group(3))]
         allocated = int(line.split()[-1])
-        expected = expected_bytes(match.group(1), ints)
+        expected = expected_bytes(match.group(1), ints, bools)
         checked += 1
         if allocated != expected:
             bad.append((match.group(1), tuple(ints), tuple(bools), allocated, expected))

@@ -419,7 +419,15 @@ __device__ __forceinline__ void dma16(rsrc_t r, const uint8_t* lds_dst, uint32_t
         static_cast<int>(voff), static_cast<int>(soff), 0, 0);
 }
 
-template <int WM, int WN, int U, int RM, int RN>
+constexpr int gcd(int a, int b) {
+    return b == 0 ? a : gcd(b, a % b);
+}
+
+constexpr int lcm(int a, int b) {
+    return a / gcd(a, b) * b;
+}
+
+template <int WM, int WN, int U, int RM, int RN, bool kDeep = false>
 struct DmaShape {
     static constexpr int kWaves = WM * WN;
     static constexpr int kThreads = kWave * kWaves;
@@ -434,14 +442,18 @@ struct DmaShape {
     // The weight ring gets one slot more (one more stage in flight) when that fits the budget and the tile
     // is already limited to that many blocks per CU: weight tiles are shared by fewer co-resident blocks
     // than activation tiles, so their loads miss L2 more often and need the longer lead.
-    static constexpr int kSlotsA = kWaves <= 4 ? 2 : 3;
+    // The deep variant (64-row tiles only, launched when all of a small grid's blocks fit on the CUs at
+    // once) keeps 3 A and 4 B slots: with one or two blocks per CU and stages of 8-16 KiB, the shallow ring
+    // has a single stage in flight and the block waits out the memory latency at every stage.
+    static constexpr int kSlotsA0 = kWaves <= 4 ? 2 : 3;
     static constexpr int kBudget = (kWaves <= 4 ? 80 : 160) * 1024;
-    static constexpr bool kDeepB = kSlotsA * kABytes + (kSlotsA + 1) * kBBytes <= kBudget &&
+    static constexpr bool kDeepB = kSlotsA0 * kABytes + (kSlotsA0 + 1) * kBBytes <= kBudget &&
                                    (kWaves > 4 || 2 * kStageBytes > 160 * 1024 / 3);
-    static constexpr int kSlotsB = kSlotsA + (kDeepB ? 1 : 0);
+    static constexpr int kSlotsA = kDeep ? 3 : kSlotsA0;
+    static constexpr int kSlotsB = kDeep ? 4 : kSlotsA0 + (kDeepB ? 1 : 0);
     static constexpr int kLeadA = kSlotsA - 1;
     static constexpr int kLeadB = kSlotsB - 1;
-    static constexpr int kPeriod = kSlotsA * kSlotsB / (kSlotsA == kSlotsB ? kSlotsA : 1);  // lcm (coprime or equal)
+    static constexpr int kPeriod = lcm(kSlotsA, kSlotsB);  // one period of both rings: compile-time slots
     static constexpr int kBRing = kSlotsA * kABytes;  // LDS offset of the B ring
     static constexpr int kLdsBytes = kSlotsA * kABytes + kSlotsB * kBBytes;
     // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two.
@@ -449,6 +461,8 @@ struct DmaShape {
     static constexpr int kAInstr = kBM * kUnitsPerRow / kWave / kWaves;   // 1 KiB direct loads per wave
     static constexpr int kBInstr = U * kBN / kWave / kWaves;
     static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
+    static_assert(!kDeep || kBM <= 64, "the deep ring is for 64-row tiles");
+    static_assert(kLeadB >= kLeadA, "the weight ring leads at least as far as the activation ring");
     static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
     static_assert(kBM * kUnitsPerRow % (kWave * kWaves) == 0, "A stage splits into whole wave loads");
     static_assert(kBN % kWave == 0 && (U * kBN / kWave) % kWaves == 0, "B stage splits into whole wave loads");
@@ -476,10 +490,12 @@ __device__ __forceinline__ int a_unit_phys(int row, int u) {
 
 // kSplitK: this launch splits K (p.splits > 1). A separate instantiation, so the unsplit kernel carries no
 // join code (its partial reads raise register pressure: measured 3% slower on a 128 x 256 tile).
-template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK>
+// kDeep: the deep-ring variant of a 64-row tile (DmaShape), chosen by the launcher for small grids.
+template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK, bool kDeep>
 __global__ __launch_bounds__(kWave * WM * WN)
-__attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN>::kWavesPerEu))) void ring_dma_kernel(const Params p) {
-    using S = DmaShape<WM, WN, U, RM, RN>;
+__attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPerEu))) void ring_dma_kernel(
+    const Params p) {
+    using S = DmaShape<WM, WN, U, RM, RN, kDeep>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
 
     const int tid = threadIdx.x;

@@ -18,6 +18,8 @@ namespace {
 constexpr bool kE5M2 = FEATHER_B_E5M2 != 0;
 constexpr bool kABf16 = FEATHER_A_BF16 != 0;
 constexpr bool kOutBf16 = FEATHER_OUT_BF16 != 0;
+constexpr int kCus = 256;                // MI355X compute units
+constexpr int kLdsPerCu = 160 * 1024;    // LDS bytes per CU
 
 template <int WM, int WN, int U, int RM, int RN, int PF>
 bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
@@ -28,12 +30,30 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
     if constexpr (PF != 0) {
         using S = DmaShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
+        const int64_t blocks = tiles * p.splits;
+        const dim3 grid(static_cast<uint32_t>(blocks));
+        if constexpr (S::kBM <= 64) {
+            // A 64-row tile takes the deep ring when every block of the launch is resident at once with it
+            // (as many blocks per CU as its LDS allows): there the deeper lead hides the memory latency that
+            // a small grid cannot hide with more blocks. Bigger grids keep the shallow ring's occupancy.
+            using D = DmaShape<WM, WN, U, RM, RN, true>;
+            if (blocks <= int64_t{kCus} * (kLdsPerCu / D::kLdsBytes)) {
+                if (p.splits > 1) {
+                    hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, true>), grid,
+                                       dim3(S::kThreads), 0, stream, p);
+                } else {
+                    hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, true>),
+                                       grid, dim3(S::kThreads), 0, stream, p);
+                }
+                return true;
+            }
+        }
         if (p.splits > 1) {
-            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true>),
-                               dim3(static_cast<uint32_t>(tiles * p.splits)), dim3(S::kThreads), 0, stream, p);
+            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, false>), grid,
+                               dim3(S::kThreads), 0, stream, p);
         } else {
-            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false>),
-                               dim3(static_cast<uint32_t>(tiles)), dim3(S::kThreads), 0, stream, p);
+            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, false>), grid,
+                               dim3(S::kThreads), 0, stream, p);
         }
     } else {
         using S = StreamShape<WM, WN, U, RM, RN>;

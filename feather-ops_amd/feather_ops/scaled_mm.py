@@ -48,9 +48,11 @@ _RING_MODEL = (
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
 _SPLIT_MIN_K = 4096
 _SPLIT_MIN_STAGES = 16
-# 32 < M <= 64: the 64 x 128 ring tile from this many tiles on, split along K to about _MID_M_RING_BLOCKS
-# workgroups.
-_MID_M_RING_TILES = 128
+# 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more (1.5 times that
+# for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on, the 64 x 64 tile below, split to
+# about _MID_M_RING_BLOCKS workgroups.
+_MID_M_RING_MIN_WEIGHT = 1 << 26
+_MID_M_WIDE_TILES = 320
 _MID_M_RING_BLOCKS = 512
 
 # The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (from
@@ -89,12 +91,15 @@ def select_scaled_mm_config(
     - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
       tiles with their measured full-grid rates).
-    - M > 64 with a smaller grid and K >= 4096: the 128 x 128 ring tile (96 tiles or more) or the
-      64 x 128 ring tile (48 or more 128 x 128 tiles), split along K (`select_scaled_mm_splits`).
+    - M > 64 with a smaller grid and K >= 4096: the 64 x 128 ring tile (deep ring) up to 256 of its
+      tiles when there are 48 or more 128 x 128 tiles, else the 128 x 128 ring tile (96 tiles or more),
+      split along K (`select_scaled_mm_splits`).
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
-    - 16 < M <= 64 with a wide N: the 64 x 128 ring tile, which reads the weight once where the 16-row
-      streaming tiles read it once per 16 rows: from 128 of its tiles when M > 32 (split along K to about
-      512 workgroups, `select_scaled_mm_splits`), from 512 when M <= 32.
+    - 16 < M <= 64 with a big weight: the 64-row ring tiles, which read the weight once where the 16-row
+      streaming tiles read it once per 16 rows (on small grids they run their deep-ring variant): from a
+      64 MB weight (N * K bytes; 96 MB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
+      the 64 x 64 tile, split along K to fill the CUs (`select_scaled_mm_splits`); for 16 < M <= 32 also
+      the 64 x 128 tile from 512 of its tiles on.
     - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
     - K >= 8192 with fewer than 192 16 x 64 streaming tiles: that tile (8 K slices per block), split along
       K across workgroups (`select_scaled_mm_splits`).
@@ -105,16 +110,17 @@ def select_scaled_mm_config(
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
         return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
+    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 48 and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
+        return _TILE_RING_64x128
     if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 96:
         return _TILE_RING_128x128
-    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 48:
-        return _TILE_RING_64x128
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
-    if 16 < M <= 64:
-        ring_tiles = _blocks(M, N, _TILE_RING_64x128)
-        if ring_tiles >= (_MID_M_RING_TILES if M > 32 else 2 * _CUS):
-            return _TILE_RING_64x128
+    if 16 < M <= 64 and N * K >= _MID_M_RING_MIN_WEIGHT * (2 if M > 32 else 3) // 2:
+        wide = _blocks(M, N, _TILE_RING_64x128) >= _MID_M_WIDE_TILES
+        return _TILE_RING_64x128 if wide else _TILE_RING_64x64
+    if 16 < M <= 32 and _blocks(M, N, _TILE_RING_64x128) >= 2 * _CUS:
+        return _TILE_RING_64x128
     if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) > 3 * _CUS // 2:
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
@@ -141,19 +147,19 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
       CU count. Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
       twelve such cells, within 4% of the best split count on most; at 224 tiles (16 x 14336 x 16384) the
       unsplit tile is faster.
-    - 32 < M <= 64 on the 64 x 128 ring tile with fewer than 512 tiles: about 512 workgroups, up to 4
-      splits of at least 16 stages. At so few rows the ring is latency-bound (each block keeps only its
-      ring's few stages in flight), and more workgroups per CU keep more of the weight in flight:
-      64 x 16384 x 4096 377 TFLOP/s split 4 ways against 188 unsplit, 64 x 32768 x 4096 517 against 361.
+    - 16 < M <= 64 on a 64-row ring tile: about 512 workgroups, 1 to 8 splits of at least 16 stages. At
+      so few rows the ring is latency-bound, and more workgroups keep more of the weight in flight:
+      64 x 16384 x 4096 414 TFLOP/s on the 64 x 64 tile split 2 ways against 360 unsplit; 64 x 5120 x
+      13824 379 split 6 ways against 130 (and 262 for the best streaming tile).
     Shorter K loses: the per-split fixed costs (pipeline fill, the partial sums' round trip through
     memory, the workspace lookup on the host) dominate.
     """
     tile = tuple(tile)
-    if tile == _TILE_RING_64x128 and 32 < M <= 64:
+    if tile in (_TILE_RING_64x128, _TILE_RING_64x64) and 16 < M <= 64:
         if tile != select_scaled_mm_config(M, N, K):
             return 1
         aim = round(_MID_M_RING_BLOCKS / _blocks(M, N, tile))
-        return max(1, min(4, aim, -(-K // 64) // _SPLIT_MIN_STAGES))
+        return max(1, min(8, aim, -(-K // 64) // _SPLIT_MIN_STAGES))
     if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
         tiles = _blocks(M, N, tile)
         if tile != select_scaled_mm_config(M, N, K) or tiles >= _STREAM_SPLIT_MAX_TILES:

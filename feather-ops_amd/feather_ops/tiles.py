@@ -16,7 +16,8 @@ Tile format: the reference's 6-tuple `(warps_m, warps_n, unroll_k, repeat_m, rep
   `16*repeat_m x 16*repeat_n` sub-tile, and K streams through LDS rings of `chunk_k`-deep stages: the
   activation ring has 2 slots for blocks of up to 4 waves (so two or three blocks share a CU) and 3 for
   8-wave blocks, and the weight ring one more when it fits (see `ring_slots`), so the next stages are in
-  flight while the current one feeds the MFMAs.
+  flight while the current one feeds the MFMAs. 64-row tiles also have a deep-ring variant (3 + 4 slots)
+  that the launcher takes for grids small enough to be resident at once (`ring_is_deep`).
 - `prefetch = 0` selects the streaming kernel for skinny M: no LDS staging. The block's `warps_m` waves
   split K instead of M (so `block_m = 16 * repeat_m`), its `warps_n` waves split N, and each wave streams
   its operands from HBM into registers `chunk_k` at a time, double-buffered; a short LDS reduction joins
@@ -63,13 +64,19 @@ def gemm_block_sizes(tile: tuple[int, ...]) -> tuple[int, int, int]:
     return block_m, 16 * warps_n * repeat_n, 16 * unroll_k
 
 
-def ring_slots(tile: tuple[int, ...]) -> tuple[int, int]:
+def ring_slots(tile: tuple[int, ...], deep: bool = False) -> tuple[int, int]:
     """(activation, weight) LDS ring slots of a `prefetch = 1` tile, the rule the kernel applies.
 
     Blocks of up to 4 waves keep 2 activation slots within an 80 KiB budget, bigger blocks 3 within
     160 KiB; the weight ring gets one more slot when that fits the budget and the tile already runs at
-    most two blocks per CU (8-wave blocks: always when it fits).
+    most two blocks per CU (8-wave blocks: always when it fits). `deep`: the deep-ring variant of a
+    64-row tile (3 and 4 slots), which the launcher takes for grids whose blocks are all resident at once
+    with it (`ring_is_deep`).
     """
+    if deep:
+        if gemm_block_sizes(tile)[0] > 64:
+            raise ValueError(f"the deep ring is for 64-row tiles: {tile}")
+        return 3, 4
     warps_m, warps_n, unroll_k, repeat_m, repeat_n = tile[:5]
     waves = warps_m * warps_n
     a_bytes = 16 * warps_m * repeat_m * unroll_k * 32
@@ -79,6 +86,23 @@ def ring_slots(tile: tuple[int, ...]) -> tuple[int, int]:
     deep_b = slots_a * a_bytes + (slots_a + 1) * b_bytes <= budget and (
         waves > 4 or 2 * (a_bytes + b_bytes) > 160 * 1024 // 3)
     return slots_a, slots_a + (1 if deep_b else 0)
+
+
+def ring_lds_bytes(tile: tuple[int, ...], deep: bool = False) -> int:
+    """LDS bytes of a ring block: its activation (2-byte) and weight (fp8) rings of `chunk_k`-deep stages."""
+    block_m, block_n, chunk_k = gemm_block_sizes(tile)
+    slots_a, slots_b = ring_slots(tile, deep)
+    return slots_a * block_m * chunk_k * 2 + slots_b * block_n * chunk_k
+
+
+def ring_is_deep(M: int, N: int, tile: tuple[int, ...], splits: int = 1) -> bool:
+    """Whether a launch of a ring tile runs the deep-ring variant (the launcher's rule): a 64-row tile
+    whose launch has no more workgroups than 256 CUs hold at once with the deep ring's LDS."""
+    block_m, block_n, _ = gemm_block_sizes(tile)
+    if tile[5] != 1 or block_m > 64:
+        return False
+    blocks = -(-M // block_m) * -(-N // block_n) * splits
+    return blocks <= 256 * (160 * 1024 // ring_lds_bytes(tile, deep=True))
 
 
 MAX_SPLITS = 32

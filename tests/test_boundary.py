@@ -203,7 +203,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
         return tile, splits(m, n, k, tile)
 
     assert auto(512, 5376, 5120) == ((2, 2, 4, 4, 4, 1), 3)     # 168 tiles -> 504 workgroups
-    assert auto(1040, 1536, 6144) == ((2, 2, 4, 4, 4, 1), 4)    # 108 tiles
+    assert auto(1040, 1536, 6144) == ((1, 4, 4, 4, 2, 1), 2)    # 204 tiles of 64 x 128 (deep ring)
     assert auto(256, 12288, 4096) == ((2, 2, 4, 4, 4, 1), 2)    # 192 tiles
     assert auto(1040, 1024, 5120) == ((1, 4, 4, 4, 2, 1), 3)    # 72 tiles of 128 x 128: 64 x 128, 136 tiles
     assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
@@ -215,21 +215,25 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 4, 0), 3)      # 64 tiles
     assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 4, 0), 3)
     assert auto(1, 8192, 28672) == ((8, 1, 4, 1, 4, 0), 2)      # 128 tiles -> 256 workgroups
-    assert auto(32, 5120, 25600) == ((8, 1, 4, 1, 4, 0), 3)     # 160 tiles (2 row blocks): 3 from 129 on
+    assert auto(16, 10240, 16384) == ((8, 1, 4, 1, 4, 0), 3)    # 160 tiles: 3 from 129 on
     assert auto(16, 2048, 8192) == ((8, 1, 4, 1, 4, 0), 4)      # 32 tiles, but K ranges of 2048 at least
     assert auto(1, 512, 65536) == ((8, 1, 4, 1, 4, 0), 8)       # at most 8
     assert auto(16, 14336, 16384) == ((8, 1, 4, 1, 4, 0), 1)    # 224 tiles: unsplit
     assert auto(8, 28672, 8192) == ((4, 1, 4, 1, 4, 0), 1)      # 448 tiles: a full grid, 4 slices, unsplit
     assert auto(16, 4096, 6144) == ((8, 1, 4, 1, 1, 0), 1)      # K < 8192: narrower tiles instead
-    assert auto(32, 25600, 8192) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
-    # 16 < M <= 64 with a wide N: the 64 x 128 ring tile, split to about 512 workgroups when M > 32
-    assert auto(64, 16384, 4096) == ((1, 4, 4, 4, 2, 1), 4)     # 128 tiles
-    assert auto(48, 32768, 4096) == ((1, 4, 4, 4, 2, 1), 2)     # 256 tiles
-    assert auto(64, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # 512 tiles
-    assert auto(64, 16384, 1024) == ((1, 4, 4, 4, 2, 1), 1)     # 16 stages: too short to split
-    assert auto(64, 8192, 4096) == ((4, 1, 4, 1, 4, 0), 1)      # 64 tiles: streaming
-    assert auto(32, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # M <= 32: from 512 tiles
-    assert auto(32, 32768, 4096) == ((2, 2, 4, 2, 2, 0), 1)     # 512 32-row tiles
+    assert auto(32, 25600, 2048) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
+    # 32 < M <= 64 with a weight of 64 MB or more: the 64-row ring tiles, split to fill the CUs
+    assert auto(64, 16384, 4096) == ((2, 2, 4, 2, 2, 1), 2)     # 256 tiles of 64 x 64 -> 512 workgroups
+    assert auto(48, 32768, 4096) == ((2, 2, 4, 2, 2, 1), 1)     # 512 tiles
+    assert auto(64, 5120, 13824) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
+    assert auto(64, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # 512 tiles of 64 x 128
+    assert auto(48, 40960, 5120) == ((1, 4, 4, 4, 2, 1), 2)     # 320 tiles of 64 x 128
+    assert auto(64, 65536, 1024) == ((1, 4, 4, 4, 2, 1), 1)
+    assert auto(64, 16384, 2048) == ((4, 1, 4, 1, 4, 0), 1)     # 32 MB weight: streaming
+    assert auto(64, 8192, 4096) == ((4, 1, 4, 1, 4, 0), 1)
+    assert auto(32, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # M <= 32: from a 96 MB weight
+    assert auto(32, 32768, 4096) == ((2, 2, 4, 2, 2, 1), 1)     # 512 tiles of 64 x 64
+    assert auto(32, 5120, 25600) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
     assert auto(32, 16384, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 256 32-row tiles: the 16-row tile
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
@@ -262,7 +266,8 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(4112, 1024, 5120) == (1, 4, 4, 4, 2, 1)    # one partial wave: 64 x 128 ring tiles
     assert pick(2304, 1280, 1280) == (2, 2, 4, 2, 2, 1)    # small grid, short K: 64 x 64 ring
     assert pick(512, 1024, 1024) == (4, 1, 4, 1, 4, 0)     # tiny grid: streaming, 4 K slices
-    assert pick(32, 25600, 5120) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
+    assert pick(32, 25600, 2048) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
+    assert pick(32, 25600, 5120) == (2, 2, 4, 2, 2, 1)     # ... and a 131 MB weight: the 64 x 64 ring tile
     assert pick(16, 14336, 4096) == (8, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 8 K slices
     assert pick(16, 4096, 4096) == (8, 1, 4, 1, 1, 0)      # narrow N: 16-column blocks for parallelism
     assert pick(16, 6144, 6144) == (8, 1, 4, 1, 2, 0)

@@ -129,17 +129,40 @@ def test_heuristic_matches_a_measured_tile(fo):
     check_against_oracle(out, a, bp, scale, None, rows=sample_rows(4112))
 
 
+@pytest.mark.parametrize("tile,m,n,deep", [
+    ((1, 4, 4, 4, 2, 1), 200, 3000, True),      # 4 x 24 tiles: the deep ring
+    ((1, 4, 4, 4, 2, 1), 4160, 1032, False),    # 65 x 9 = 585 tiles: more than 512, the shallow ring
+    ((2, 2, 4, 2, 2, 1), 130, 1000, True),
+    ((2, 2, 4, 2, 2, 1), 4160, 1032, False),    # 65 x 17 = 1105 tiles: more than 1024
+])
+@pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
+def test_deep_and_shallow_ring_variants(fo, tile, m, n, deep, a_dtype):
+    """A 64-row ring tile runs its deep-ring instantiation on grids whose blocks are all resident at once and
+    the shallow one beyond; both against the oracle, bf16 activations included (register-staged path)."""
+    from feather_ops.tiles import ring_is_deep
+
+    assert ring_is_deep(m, n, tile) == deep
+    K = 1040
+    a = _tensor((m, K), a_dtype)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, n), torch.float8_e4m3fn, seed=1))
+    s = torch.tensor(0.25, device="cuda")
+    bias = _tensor((n,), torch.bfloat16, seed=2)
+    out = fo.scaled_mm_hip(a, bp, s, bias, torch.bfloat16, tile=tile)
+    check_against_oracle(out, a, bp, s, bias, rows=None if m < 1000 else sample_rows(m, n_random=16))
+
+
 # One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, split
-# across workgroups for long K, the 32-row streaming tile, the 64 x 128 ring tile for 16 < M <= 64 with a
-# wide N, split or not, the 64 x 64 ring tile for mid-size grids, and the
+# across workgroups for long K, the 32-row streaming tile, the 64-row ring tiles for 16 < M <= 64 with a
+# big weight, split or not, the 64 x 64 ring tile for mid-size grids, and the
 # wave-quantization choice among 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out
 # with a bias, against the oracle.
 HEURISTIC_CELLS = [
     (2, 4096, 16384),    # 16 x 64 streaming tile split 3 ways along K across workgroups
     (16, 4096, 4096),    # 16 x 16 columns, 8 slices
     (16, 6144, 6144),    # 16 x 32 columns
-    (32, 25600, 5120),   # 32-row streaming tile
-    (64, 16384, 4096),   # 64 x 128 ring tile at 64 rows, split 4 ways along K
+    (32, 25600, 2048),   # 32-row streaming tile
+    (32, 5120, 25600),   # 64 x 64 ring tile at 32 rows, split 6 ways along K (deep ring)
+    (64, 16384, 4096),   # 64 x 64 ring tile at 64 rows (deep ring), split 2 ways along K
     (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
     (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K

@@ -5,6 +5,8 @@ import pathlib
 import subprocess
 import sys
 
+import pytest
+
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 
@@ -57,6 +59,26 @@ def test_ring_slots_rule():
     assert ring_slots((2, 2, 4, 4, 4, 1)) == (2, 2)  # 128 x 128: keeps three blocks per CU
     assert ring_slots((2, 2, 4, 8, 4, 1)) == (2, 2)  # 256 x 128: 2 x 32 + 3 x 8 KiB exceeds 80 KiB
     assert ring_slots((4, 2, 4, 4, 8, 1)) == (3, 4)  # 256 x 256, 8 waves: 96 + 64 KiB
+    assert ring_slots((1, 4, 4, 4, 2, 1)) == (2, 2)  # 64 x 128: 8 KiB stages, up to four blocks per CU
+    assert ring_slots((1, 4, 4, 4, 2, 1), deep=True) == (3, 4)  # its deep variant: 56 KiB
+    with pytest.raises(ValueError):
+        ring_slots((2, 2, 4, 4, 4, 1), deep=True)  # 128 rows: no deep variant
+
+
+def test_deep_ring_rule():
+    """The launcher's choice: a 64-row tile's launch takes the deep ring when all its workgroups are resident
+    at once with it (64 x 128: 56 KiB, 2 blocks per CU -> 512; 64 x 64: 40 KiB, 4 per CU -> 1024)."""
+    from feather_ops.tiles import ring_is_deep, ring_lds_bytes
+
+    assert ring_lds_bytes((1, 4, 4, 4, 2, 1), deep=True) == 56 * 1024
+    assert ring_lds_bytes((2, 2, 4, 2, 2, 1), deep=True) == 40 * 1024
+    assert ring_is_deep(64, 65536, (1, 4, 4, 4, 2, 1))           # 512 tiles
+    assert not ring_is_deep(64, 65536 + 128, (1, 4, 4, 4, 2, 1))
+    assert ring_is_deep(64, 16384, (1, 4, 4, 4, 2, 1), splits=4)  # 128 tiles x 4
+    assert not ring_is_deep(64, 16384, (1, 4, 4, 4, 2, 1), splits=5)
+    assert ring_is_deep(2304, 1280, (2, 2, 4, 2, 2, 1))          # 720 tiles of 64 x 64
+    assert not ring_is_deep(64, 1024, (2, 2, 4, 4, 4, 1))        # 128 rows
+    assert not ring_is_deep(16, 1024, (8, 1, 4, 1, 4, 0))        # streaming
 
 
 def test_tile_shape_formula():
@@ -78,10 +100,9 @@ def _check_lds():
 
 def test_every_kernel_allocates_exactly_its_tiles_lds():
     """The LDS audit (check_lds.py, the reference's tools/check_lds.py role): the compiled gfx950 code
-    object's group_segment_fixed_size of every ring and streaming instantiation (unsplit and split) equals
-    the size the tile asks for. Compiles one dtype combination (hipcc, device code only)."""
-    import pytest
-
+    object's group_segment_fixed_size of every ring (unsplit and split, shallow and, for 64-row tiles, deep)
+    and streaming instantiation (unsplit and split) equals the size the tile asks for. Compiles one dtype
+    combination (hipcc, device code only)."""
     from feather_ops.tiles import SCALED_MM_TILES
 
     check = _check_lds()
@@ -89,11 +110,13 @@ def test_every_kernel_allocates_exactly_its_tiles_lds():
         pytest.skip("needs hipcc")
     asm = check.compile_asm("100")
     checked, bad = check.audit(asm)
-    assert checked == 2 * len(SCALED_MM_TILES)
+    small_ring = sum(1 for t in SCALED_MM_TILES if t[5] == 1 and 16 * t[0] * t[3] <= 64)
+    assert small_ring == 2
+    assert checked == 2 * len(SCALED_MM_TILES) + 2 * small_ring
     assert bad == []
     # a planted off-by-one in the expectation is caught for every instantiation
     real = check.expected_bytes
-    check.expected_bytes = lambda kernel, ints: real(kernel, ints) + 1
+    check.expected_bytes = lambda kernel, ints, bools=(): real(kernel, ints, bools) + 1
     try:
         assert len(check.audit(asm)[1]) == checked
     finally:
