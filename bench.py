@@ -204,12 +204,21 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
 
     c3 / c4: the scaled_mm kernel on that cell (c4 rotates over 8 weight copies); copy: torch's
     device-to-device copy of a 512 MiB buffer, whose FETCH_SIZE / WRITE_SIZE calibrate the counters
-    (1 x 512 MiB read and 1 x 512 MiB written per launch).
+    (1 x 512 MiB read and 1 x 512 MiB written per launch); torch_c3: torch's fp16 matmul (hipBLASLt) on
+    the C3 shape with the weight already dequantized to fp16, the library control a counter comparison
+    is made against.
     """
     import torch
 
     import feather_ops
 
+    if which == "torch_c3":
+        a = torch.randn(4096, 3072, device="cuda", dtype=torch.float16)
+        w = torch.randn(12288, 3072, device="cuda", dtype=torch.float16)
+        for _ in range(warmup + steps):
+            torch.mm(a, w.t())
+        torch.cuda.synchronize()
+        return
     if which == "copy":
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
@@ -269,7 +278,8 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the C4 (HBM), C2 (bf16) and split-K cells")
-    parser.add_argument("--only", choices=["c3", "c4", "copy"], help="launch one kernel only (for profilers)")
+    parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3"],
+                        help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
