@@ -100,6 +100,9 @@ def select_scaled_mm_config(
       64 MB weight (N * K bytes; 96 MB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
       the 64 x 64 tile, split along K to fill the CUs (`select_scaled_mm_splits`); for 16 < M <= 32 also
       the 64 x 128 tile from 512 of its tiles on.
+    - M <= 16 with 512 to 1024 64 x 128 tiles (N from 65536 to 131072, LM-head widths): that ring tile,
+      whose direct-to-LDS weight stream runs 5-12% faster than the streaming tiles there; beyond 1024
+      tiles the second, partial wave of blocks makes it slower.
     - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
     - K >= 8192 with fewer than 192 16 x 64 streaming tiles: that tile (8 K slices per block), split along
       K across workgroups (`select_scaled_mm_splits`).
@@ -119,8 +122,10 @@ def select_scaled_mm_config(
     if 16 < M <= 64 and N * K >= _MID_M_RING_MIN_WEIGHT * (2 if M > 32 else 3) // 2:
         wide = _blocks(M, N, _TILE_RING_64x128) >= _MID_M_WIDE_TILES
         return _TILE_RING_64x128 if wide else _TILE_RING_64x64
-    if 16 < M <= 32 and _blocks(M, N, _TILE_RING_64x128) >= 2 * _CUS:
-        return _TILE_RING_64x128
+    if M <= 32:
+        ring_tiles = _blocks(M, N, _TILE_RING_64x128)
+        if ring_tiles >= 2 * _CUS and (M > 16 or ring_tiles <= 4 * _CUS):
+            return _TILE_RING_64x128
     if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) > 3 * _CUS // 2:
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:

@@ -271,4 +271,6 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(16, 14336, 4096) == (8, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 8 K slices
     assert pick(16, 4096, 4096) == (8, 1, 4, 1, 1, 0)      # narrow N: 16-column blocks for parallelism
     assert pick(16, 6144, 6144) == (8, 1, 4, 1, 2, 0)
-    assert pick(1, 96768, 2688) == (4, 1, 4, 1, 4, 0)      # one row, very wide: many blocks, 4 slices
+    assert pick(1, 96768, 2688) == (1, 4, 4, 4, 2, 1)      # one row, LM-head width: 756 ring tiles
+    assert pick(1, 151936, 3584) == (4, 1, 4, 1, 4, 0)     # 1187 ring tiles: a partial second wave
+    assert pick(1, 32000, 4096) == (4, 1, 4, 1, 4, 0)      # 250 ring tiles: streaming
