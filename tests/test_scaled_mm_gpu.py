@@ -164,6 +164,7 @@ HEURISTIC_CELLS = [
     (32, 5120, 25600),   # 64 x 64 ring tile at 32 rows, split 6 ways along K (deep ring)
     (64, 16384, 4096),   # 64 x 64 ring tile at 64 rows (deep ring), split 2 ways along K
     (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit
+    (1, 96768, 2688),    # 64 x 128 ring tile at one row, an LM-head width (756 tiles)
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
     (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
     (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways
