@@ -129,25 +129,29 @@ def test_heuristic_matches_a_measured_tile(fo):
     check_against_oracle(out, a, bp, scale, None, rows=sample_rows(4112))
 
 
-@pytest.mark.parametrize("tile,m,n,deep", [
-    ((1, 4, 4, 4, 2, 1), 200, 3000, True),      # 4 x 24 tiles: the deep ring
-    ((1, 4, 4, 4, 2, 1), 4160, 1032, False),    # 65 x 9 = 585 tiles: more than 512, the shallow ring
-    ((2, 2, 4, 2, 2, 1), 130, 1000, True),
-    ((2, 2, 4, 2, 2, 1), 4160, 1032, False),    # 65 x 17 = 1105 tiles: more than 1024
+@pytest.mark.parametrize("tile,m,n,splits,deep", [
+    ((1, 4, 4, 4, 2, 1), 200, 3000, 1, True),      # 4 x 24 tiles: the deep ring
+    ((1, 4, 4, 4, 2, 1), 4160, 1032, 1, False),    # 65 x 9 = 585 tiles: more than 512, the shallow ring
+    ((2, 2, 4, 2, 2, 1), 130, 1000, 1, True),
+    ((2, 2, 4, 2, 2, 1), 4160, 1032, 1, False),    # 65 x 17 = 1105 tiles: more than 1024
+    ((1, 4, 4, 4, 2, 1), 200, 3000, 4, True),      # 96 tiles x 4 splits
+    ((1, 4, 4, 4, 2, 1), 1040, 4104, 2, False),    # 17 x 33 tiles x 2 splits = 1122 workgroups
+    ((2, 2, 4, 2, 2, 1), 2112, 1032, 2, False),    # 33 x 17 tiles x 2 splits = 1122 workgroups
 ])
 @pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
-def test_deep_and_shallow_ring_variants(fo, tile, m, n, deep, a_dtype):
-    """A 64-row ring tile runs its deep-ring instantiation on grids whose blocks are all resident at once and
-    the shallow one beyond; both against the oracle, bf16 activations included (register-staged path)."""
+def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
+    """A 64-row ring tile runs its deep-ring instantiation on grids whose workgroups are all resident at once
+    and the shallow one beyond, split or not; each against the oracle, bf16 activations included (the
+    register-staged path)."""
     from feather_ops.tiles import ring_is_deep
 
-    assert ring_is_deep(m, n, tile) == deep
+    assert ring_is_deep(m, n, tile, splits) == deep
     K = 1040
     a = _tensor((m, K), a_dtype)
     bp = fo.prepack_b_for_scaled_mm(_tensor((K, n), torch.float8_e4m3fn, seed=1))
     s = torch.tensor(0.25, device="cuda")
     bias = _tensor((n,), torch.bfloat16, seed=2)
-    out = fo.scaled_mm_hip(a, bp, s, bias, torch.bfloat16, tile=tile)
+    out = fo.scaled_mm_hip(a, bp, s, bias, torch.bfloat16, tile=tile, splits=splits)
     check_against_oracle(out, a, bp, s, bias, rows=None if m < 1000 else sample_rows(m, n_random=16))
 
 
