@@ -276,11 +276,19 @@ def scaled_mm_hip(
     `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it. `splits` (not in the
     reference) pins the split-K count; by default the heuristic picks it when `tile` is None and a pinned
     tile runs unsplit.
+
+    The heuristic's launch goes through the opaque custom op `feather_ops::scaled_mm_auto` while
+    `torch.compile` traces (as in the reference, `scaled_mm.py:104-134`), and straight to the launcher in
+    eager mode: the same launch without the custom op's Python dispatch, about 7 us of host time per call,
+    which is more than a decode-sized kernel takes.
     """
     _lib.require_native()
     out = torch.empty((a.shape[0], b_prepacked.shape[1]), device=a.device, dtype=out_dtype)
     if tile is None and splits is None:
-        _scaled_mm_auto(a, b_prepacked, scale, bias, out)
+        if torch.compiler.is_compiling():
+            _scaled_mm_auto(a, b_prepacked, scale, bias, out)
+        else:
+            _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1]))
     else:
         if tile is None:
             tile = select_scaled_mm_config(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype,

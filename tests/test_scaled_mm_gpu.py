@@ -346,6 +346,27 @@ def test_compile_matches_eager(fo, m, n, k):
         assert torch.equal(compiled.view(torch.int16), eager.view(torch.int16))
 
 
+def test_compiled_graph_holds_the_opaque_auto_op(fo):
+    """Under torch.compile the auto path is the custom op `feather_ops::scaled_mm_auto` (one node, the
+    heuristic not traced into the graph), while eager calls skip the op's Python dispatch."""
+    graphs = []
+
+    def backend(gm, example_inputs):
+        graphs.append(gm)
+        return gm.forward
+
+    a = _tensor((64, 256), torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((256, 128), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.5, device="cuda")
+    torch._dynamo.reset()
+    out = torch.compile(lambda a, bp, s: fo.scaled_mm_hip(a, bp, s, None, torch.float16), backend=backend,
+                        fullgraph=True)(a, bp, s)
+    targets = [node.target for gm in graphs for node in gm.graph.nodes if node.op == "call_function"]
+    assert torch.ops.feather_ops.scaled_mm_auto.default in targets, targets
+    assert not any("scaled_mm.default" in str(t) and "auto" not in str(t) for t in targets)
+    assert torch.equal(out.view(torch.int16), fo.scaled_mm_hip(a, bp, s, None, torch.float16).view(torch.int16))
+
+
 # ---- empty and maximum sizes ----------------------------------------------------------------------------------
 
 def test_empty_m_returns_an_empty_output(fo):
