@@ -50,6 +50,19 @@ def test_forward_matches_the_kernel_and_the_oracle(fo, fp8, per_channel, dtype, 
     assert rel < (0.08 if fp8 == torch.float8_e5m2 else 0.04), rel
 
 
+def test_inference_path_matches_the_op(fo):
+    """Under no_grad the layer skips the custom op's dispatch; the output is the op's bit for bit."""
+    lin = _linear(512, 320)
+    fo.to_scaled_mm_linear(lin, torch.float8_e4m3fn, per_channel=True)
+    x = torch.randn(5, 7, 512, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        fast = lin(x)
+    via_op = torch.ops.feather_ops.scaled_mm_linear(x, lin.weight_fp8, lin.weight_scale, lin.bias.to(x.dtype))
+    assert torch.equal(fast.view(torch.int16), via_op.view(torch.int16))
+    with torch.inference_mode():
+        assert torch.equal(lin(x).view(torch.int16), via_op.view(torch.int16))
+
+
 def test_misaligned_input_view(fo):
     """An input view that starts 2 bytes into its buffer is copied once, not refused."""
     lin = _linear(256, 128)
