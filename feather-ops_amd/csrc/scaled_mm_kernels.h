@@ -105,24 +105,13 @@ __device__ __forceinline__ void e5m2x4_to_f16(uint32_t p, uint32_t& lo, uint32_t
     hi = __builtin_amdgcn_perm(0u, p, perm_sel(kZeroByte, 2, kZeroByte, 3));
 }
 
-// e4m3fn -> fp16, exact. The 7 magnitude bits (eeee mmm) placed at fp16 bits 13..7 form an fp16 whose
-// value is exactly |x| / 256 for every finite code: a normal code is 2^(e-7) (1 + m/8) and reads as
-// 2^(e-15) (1 + m/8); a subnormal code is m 2^-9 and reads as the fp16 subnormal (m << 7) 2^-24 = m 2^-17.
-// One exact fp16 multiply by 256 restores |x|, the sign is or-ed back, and the one NaN magnitude (0x7f)
-// becomes an fp16 NaN.
-__device__ __forceinline__ uint32_t e4m3x2_to_f16(uint32_t pair /* bytes in bits 7..0 and 23..16 */) {
-    const uint32_t mag = (pair & 0x007f007fu) << 7;
-    half2v h = __builtin_bit_cast(half2v, mag);
-    h = h * half2v{static_cast<_Float16>(256.0f), static_cast<_Float16>(256.0f)};
-    uint32_t r = __builtin_bit_cast(uint32_t, h) | ((pair & 0x00800080u) << 8);
-    if ((pair & 0x7fu) == 0x7fu) r = (r & 0xffff0000u) | 0x7e00u;
-    if ((pair & 0x007f0000u) == 0x007f0000u) r = (r & 0x0000ffffu) | 0x7e000000u;
-    return r;
-}
-
+// e4m3fn -> fp16, exact: every e4m3fn value (normals 2^-6 .. 448, subnormals m 2^-9) is an fp16 normal,
+// so gfx950's fp8 -> fp16 conversion at scale 1 (v_cvt_scalef32_pk_f16_fp8: the two codes of one 16-bit
+// word per instruction) is exact, and the NaN codes 0x7f / 0xff convert to fp16 NaNs. One instruction per
+// two codes, against ten bit operations and an fp16 multiply for the same exact result by hand.
 __device__ __forceinline__ void e4m3x4_to_f16(uint32_t p, uint32_t& lo, uint32_t& hi) {
-    lo = e4m3x2_to_f16(__builtin_amdgcn_perm(0u, p, perm_sel(0, kZeroByte, 1, kZeroByte)));
-    hi = e4m3x2_to_f16(__builtin_amdgcn_perm(0u, p, perm_sel(2, kZeroByte, 3, kZeroByte)));
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(p, 1.0f, false));
+    hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(p, 1.0f, true));
 }
 
 // 16 weight bytes (16 consecutive k of one column) -> the two 8-wide fp16 MFMA operands.

@@ -231,18 +231,22 @@ def test_baseline_config(fo, name):
 
 # ---- edge cases --------------------------------------------------------------------------------------------
 
-def test_specials_propagate_like_the_oracle(fo):
+@pytest.mark.parametrize("fp8,specials", [(torch.float8_e5m2, (0x7C, 0x7E)),      # +inf, NaN
+                                          (torch.float8_e4m3fn, (0x7F, 0xFF))])   # the two NaN codes
+@pytest.mark.parametrize("tile", [None, (2, 2, 4, 4, 4, 1), (8, 1, 4, 1, 4, 0)])
+def test_specials_propagate_like_the_oracle(fo, fp8, specials, tile):
     g = torch.Generator("cpu").manual_seed(9)
     a = torch.randn(20, 64, generator=g).to(torch.float16)
     a[3, 5] = float("inf")
     a[7, 9] = float("nan")
-    codes = torch.randn(64, 24, generator=g).to(torch.float8_e5m2).view(torch.uint8)
-    codes[11, 4] = 0x7C  # +inf
-    codes[13, 17] = 0x7E  # NaN
-    bp = fo.prepack_b_for_scaled_mm(codes.view(torch.float8_e5m2).cuda())
+    codes = torch.randn(64, 24, generator=g).to(fp8).view(torch.uint8)
+    codes[11, 4] = specials[0]
+    codes[13, 17] = specials[1]
+    bp = fo.prepack_b_for_scaled_mm(codes.view(fp8).cuda())
     for out_dtype in (torch.float16, torch.bfloat16):
-        out = fo.scaled_mm_hip(a.cuda(), bp, torch.tensor(0.5, device="cuda"), None, out_dtype)
+        out = fo.scaled_mm_hip(a.cuda(), bp, torch.tensor(0.5, device="cuda"), None, out_dtype, tile=tile)
         check_against_oracle(out, a.cuda(), bp, torch.tensor(0.5), None)
+        assert torch.isnan(out[:, 17]).all()
 
 
 def test_bf16_activation_past_fp16_range_becomes_inf_like_naive(fo):
@@ -274,6 +278,26 @@ def test_e4m3fn_all_codes(fo):
     bp = fo.prepack_b_for_scaled_mm(codes.view(torch.float8_e4m3fn).cuda())
     out = fo.scaled_mm_hip(a.cuda(), bp, None, None, torch.float16)
     check_against_oracle(out, a.cuda(), bp, None, None)
+
+
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("tile", [(2, 2, 4, 4, 4, 1), (2, 2, 4, 2, 2, 1), (8, 1, 4, 1, 4, 0), (4, 1, 4, 1, 1, 0)])
+def test_decode_is_exact_on_every_finite_code(fo, fp8, tile):
+    """An identity activation copies the decoded weight to the output (one product per element, exact in
+    fp32 and in the fp16 output), so the output must equal torch's fp8 -> fp16 cast for every finite code,
+    in the ring and the streaming kernel alike: the same fp16 value (so the same bits, except that the
+    -0 code sums to +0 with the other rows' zero products)."""
+    k = 256
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(k, 1).repeat(1, 16)
+    special = 0x7F if fp8 == torch.float8_e4m3fn else 0x7C
+    codes[codes & special == special] = 0x38  # inf / NaN codes would poison every row through 0 * x
+    w = codes.view(fp8)
+    a = torch.eye(k, dtype=torch.float16).cuda()
+    out = fo.scaled_mm_hip(a, fo.prepack_b_for_scaled_mm(w.cuda()), None, None, torch.float16, tile=tile)
+    want = w.to(torch.float16)
+    assert torch.equal(out.cpu(), want)
+    nonzero = want != 0
+    assert torch.equal(out.cpu().view(torch.int16)[nonzero], want.view(torch.int16)[nonzero])
 
 
 def test_deterministic(fo):
