@@ -270,6 +270,21 @@ def test_subnormal_weights_and_activations(fo):
     check_against_oracle(out, a.cuda(), bp, s.cpu(), None)
 
 
+@pytest.mark.parametrize("tile", [None, (2, 2, 4, 4, 4, 1), (8, 1, 4, 1, 4, 0)])
+def test_bf16_output_subnormals_and_rounding(fo, tile):
+    """bf16 outputs round to nearest even through the whole fp32 range: a scale of 2^-130 puts the results
+    among bf16's subnormals, where a flush to zero or a truncation would show."""
+    g = torch.Generator("cpu").manual_seed(12)
+    a = torch.randn(40, 256, generator=g).to(torch.float16)
+    bp = fo.prepack_b_for_scaled_mm(torch.randn(256, 72, generator=g).to(torch.float8_e5m2).cuda())
+    for s in (2.0**-130, 2.0**-120, 0.37):
+        scale = torch.tensor(s, device="cuda")
+        out = fo.scaled_mm_hip(a.cuda(), bp, scale, None, torch.bfloat16, tile=tile)
+        check_against_oracle(out, a.cuda(), bp, scale, None)
+        if s == 2.0**-130:
+            assert (out != 0).float().mean().item() > 0.9  # not flushed
+
+
 def test_e4m3fn_all_codes(fo):
     k = 256
     codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(k, 1).repeat(1, 16)
