@@ -47,10 +47,10 @@ def algorithmic_bytes(m: int, k: int, n: int, bias: bool = False) -> int:
     return 2 * m * k + k_pad * n + 2 * m * n + 4 + (2 * n if bias else 0)
 
 
-def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0):
+def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0, fp8="e5m2"):
     """The benchmark workload, generated on the GPU: A ~ N(0, 1) [M, K] in fp16 or bf16, W ~ N(0, 0.02)
-    [N, K] quantized to e5m2 with the per-tensor scale max|W| / 57344, prepacked by the package's own
-    `prepack_b_for_scaled_mm`. Returns (a, [prepacked weight x copies], scale)."""
+    [N, K] quantized to e5m2 (or e4m3fn) with the per-tensor scale max|W| / 57344 (448), prepacked by the
+    package's own `prepack_b_for_scaled_mm`. Returns (a, [prepacked weight x copies], scale)."""
     import torch
 
     import feather_ops
@@ -60,8 +60,9 @@ def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0):
     a_dtype = torch.bfloat16 if a_fmt == "bf16" else torch.float16
     a = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float32).to(a_dtype)
     w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
-    scale = w.abs().max() / 57344.0
-    w8 = (w / scale).to(torch.float8_e5m2)
+    fp8_dtype, fp8_max = (torch.float8_e4m3fn, 448.0) if fp8 == "e4m3fn" else (torch.float8_e5m2, 57344.0)
+    scale = w.abs().max() / fp8_max
+    w8 = (w / scale).to(fp8_dtype)
     del w
     b0 = feather_ops.prepack_b_for_scaled_mm(w8.t().contiguous())
     del w8
@@ -96,6 +97,31 @@ def time_c3(steps: int, warmup: int):
     flops = 2.0 * m * n * k
     return {"m": m, "k": k, "n": n, "tile": list(tile), "ms": ms, "wall_s": wall, "tflops": flops / (ms * 1e-3) / 1e12,
             "bytes": algorithmic_bytes(m, k, n)}
+
+
+def time_e4m3_cell(steps: int = 100, warmup: int = 10):
+    """The C3 shape with e4m3fn weights (the other fp8 format the API takes), timed like C3."""
+    import torch
+
+    import feather_ops
+
+    m, k, n = 4096, 3072, 12288
+    a, bs, s = make_device_inputs(m, k, n, "fp16", fp8="e4m3fn")
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
+    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    op = torch.ops.feather_ops.scaled_mm.default
+    for _ in range(warmup):
+        op(a, bs[0], s, None, out, *tile)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        op(a, bs[0], s, None, out, *tile)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
 
 
 def time_c4(reps: int = 50, copies: int = 8):
@@ -277,7 +303,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     parser.add_argument("--no-secondary", action="store_true",
-                        help="skip the C4 (HBM), C2 (bf16) and split-K cells")
+                        help="skip the C4 (HBM), C2 (bf16), e4m3fn and split-K cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3"],
                         help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
@@ -301,6 +327,7 @@ def main() -> int:
     c4 = None if args.no_secondary else time_c4()
     c2 = None if args.no_secondary else time_c2()
     # 168 tiles of 128 x 128 for 256 CUs; the unsplit control is the best unsplit tile of the sweep
+    e4 = None if args.no_secondary else time_e4m3_cell()
     sk = None if args.no_secondary else time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1))
     # a decoder's down projection at batch 2: 64 tiles of 16 x 64, 67 MB of weight, 8 rotated copies; the
     # unsplit control is the streaming tile the heuristic picks without split-K (16 x 16, 256 blocks)
@@ -337,6 +364,10 @@ def main() -> int:
         line["bf16_cell"] = {"workload": "C2 DiT attention projection: bf16 [4096,3072] x e5m2 [3072,3072] -> bf16",
                              "TFLOPs": round(c2["tflops"], 1), "us_per_launch": round(c2["us"], 2),
                              "frac_fp16_peak": round(c2["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": c2["tile"]}
+    if e4 is not None:
+        line["e4m3_cell"] = {"workload": "C3 shape with e4m3fn weights: fp16 [4096,3072] x e4m3fn [12288,3072] -> fp16",
+                             "TFLOPs": round(e4["tflops"], 1), "us_per_launch": round(e4["us"], 2),
+                             "frac_fp16_peak": round(e4["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": e4["tile"]}
     if sk is not None:
         line["splitk_cell"] = {"workload": "underfilled grid: fp16 [512,5120] x e5m2 [5376,5120] -> fp16",
                                "tile": sk["tile"], "splits": sk["splits"],
