@@ -552,8 +552,11 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
     // registers (load_a) and widened to fp16 once per block when written to LDS (commit_a), so the operand
     // reads need no conversion and no element is widened twice (measured ~9% faster on 4096x3072x3072).
     // 8-wave blocks keep the deeper direct-load ring for bf16 too and widen per fragment (register staging
-    // shortens their activation lead from two stages to one and measured 11% slower).
-    constexpr bool kStageA = kABf16 && S::kWaves <= 4;
+    // shortens their activation lead from two stages to one and measured 11% slower), and so does the deep
+    // ring (launched for bf16 only at M <= 64 on tiles of at most two column waves): its small grids are
+    // latency-bound, and a one-stage activation lead undid the deep ring (32x5120x25600 on the 64 x 64
+    // tile: 106 TFLOP/s staged, 235 widened per fragment).
+    constexpr bool kStageA = kABf16 && S::kWaves <= 4 && !kDeep;
     u32x4 a_regs[S::kAInstr];
     auto load_a = [&](int local_stage) {
         const int stage = stage0 + local_stage;

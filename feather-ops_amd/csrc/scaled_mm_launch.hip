@@ -32,12 +32,14 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         const int64_t blocks = tiles * p.splits;
         const dim3 grid(static_cast<uint32_t>(blocks));
-        if constexpr (S::kBM <= 64) {
+        if constexpr (S::kBM <= 64 && (!kABf16 || WN <= 2)) {
             // A 64-row tile takes the deep ring when every block of the launch is resident at once with it
             // (as many blocks per CU as its LDS allows): there the deeper lead hides the memory latency that
             // a small grid cannot hide with more blocks. Bigger grids keep the shallow ring's occupancy.
+            // With bf16 activations the deep ring widens per fragment (each of the WN column waves widens
+            // the block's rows again), which pays only while M <= 64 and WN <= 2.
             using D = DmaShape<WM, WN, U, RM, RN, true>;
-            if (blocks <= int64_t{kCus} * (kLdsPerCu / D::kLdsBytes)) {
+            if ((!kABf16 || p.M <= 64) && blocks <= int64_t{kCus} * (kLdsPerCu / D::kLdsBytes)) {
                 if (p.splits > 1) {
                     hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, true>), grid,
                                        dim3(S::kThreads), 0, stream, p);

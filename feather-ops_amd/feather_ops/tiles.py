@@ -95,11 +95,15 @@ def ring_lds_bytes(tile: tuple[int, ...], deep: bool = False) -> int:
     return slots_a * block_m * chunk_k * 2 + slots_b * block_n * chunk_k
 
 
-def ring_is_deep(M: int, N: int, tile: tuple[int, ...], splits: int = 1) -> bool:
+def ring_is_deep(M: int, N: int, tile: tuple[int, ...], splits: int = 1, a_bf16: bool = False) -> bool:
     """Whether a launch of a ring tile runs the deep-ring variant (the launcher's rule): a 64-row tile
-    whose launch has no more workgroups than 256 CUs hold at once with the deep ring's LDS."""
+    whose launch has no more workgroups than 256 CUs hold at once with the deep ring's LDS; with bf16
+    activations (widened per fragment in the deep ring) only while M <= 64 and the tile has at most two
+    column waves."""
     block_m, block_n, _ = gemm_block_sizes(tile)
     if tile[5] != 1 or block_m > 64:
+        return False
+    if a_bf16 and (M > 64 or tile[1] > 2):
         return False
     blocks = -(-M // block_m) * -(-N // block_n) * splits
     return blocks <= 256 * (160 * 1024 // ring_lds_bytes(tile, deep=True))

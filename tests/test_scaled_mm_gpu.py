@@ -137,6 +137,7 @@ def test_heuristic_matches_a_measured_tile(fo):
     ((1, 4, 4, 4, 2, 1), 200, 3000, 4, True),      # 96 tiles x 4 splits
     ((1, 4, 4, 4, 2, 1), 1040, 4104, 2, False),    # 17 x 33 tiles x 2 splits = 1122 workgroups
     ((2, 2, 4, 2, 2, 1), 2112, 1032, 2, False),    # 33 x 17 tiles x 2 splits = 1122 workgroups
+    ((2, 2, 4, 2, 2, 1), 48, 3000, 3, True),       # bf16 activations too: M <= 64, two column waves
 ])
 @pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
 def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
@@ -146,6 +147,8 @@ def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
     from feather_ops.tiles import ring_is_deep
 
     assert ring_is_deep(m, n, tile, splits) == deep
+    if a_dtype == torch.bfloat16:
+        deep = ring_is_deep(m, n, tile, splits, a_bf16=True)
     K = 1040
     a = _tensor((m, K), a_dtype)
     bp = fo.prepack_b_for_scaled_mm(_tensor((K, n), torch.float8_e4m3fn, seed=1))

@@ -79,6 +79,10 @@ def test_deep_ring_rule():
     assert ring_is_deep(2304, 1280, (2, 2, 4, 2, 2, 1))          # 720 tiles of 64 x 64
     assert not ring_is_deep(64, 1024, (2, 2, 4, 4, 4, 1))        # 128 rows
     assert not ring_is_deep(16, 1024, (8, 1, 4, 1, 4, 0))        # streaming
+    # bf16 activations: only at M <= 64 and with at most two column waves (per-fragment widening)
+    assert ring_is_deep(64, 16384, (2, 2, 4, 2, 2, 1), a_bf16=True)
+    assert not ring_is_deep(130, 1000, (2, 2, 4, 2, 2, 1), a_bf16=True)
+    assert not ring_is_deep(64, 16384, (1, 4, 4, 4, 2, 1), a_bf16=True)
 
 
 def test_tile_shape_formula():
