@@ -54,6 +54,7 @@ def _blocks(m: int, n: int, tile: tuple[int, ...]) -> int:
     return -(-m // bm) * -(-n // bn)
 
 _DT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+_FP8 = {"e5m2": torch.float8_e5m2, "e4m3fn": torch.float8_e4m3fn}
 
 
 def parse_tiles(text: str) -> list[tuple[int, ...]]:
@@ -83,7 +84,8 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
     a = torch.randn((m, k), generator=gen, device="cuda").to(a_dtype)
-    b_kn = torch.randn((k, n), generator=gen, device="cuda").to(torch.float8_e5m2)
+    fp8 = _FP8[args.fp8]
+    b_kn = torch.randn((k, n), generator=gen, device="cuda").to(fp8)
     scale = torch.tensor(2.34, device="cuda", dtype=torch.float32)
     bias = torch.randn(n, generator=gen, device="cuda").to(out_dtype) if args.bias else None
     copies = weight_copies(n, k, args.cold)
@@ -95,7 +97,7 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     out = torch.empty((m, n), device="cuda", dtype=out_dtype)
     op = torch.ops.feather_ops.scaled_mm.default
 
-    picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, out_dtype))
+    picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, fp8, out_dtype))
     picked_splits = select_scaled_mm_splits(m, n, k, picked)
     split_cases = [(tile, splits) for tile in tiles for splits in args.splits
                    if (_blocks(m, n, tile) < _CUS or args.split_any_grid) and _blocks(m, n, tile) * splits <= 4 * _CUS
@@ -148,6 +150,7 @@ def main() -> int:
                         help="time the split counts on grids of a CU's worth of tiles or more too")
     parser.add_argument("--a-dtype", choices=list(_DT), default="bf16")
     parser.add_argument("--out-dtype", choices=list(_DT), default="bf16")
+    parser.add_argument("--fp8", choices=list(_FP8), default="e5m2", help="weight format")
     parser.add_argument("--no-bias", dest="bias", action="store_false")
     parser.add_argument("--cold", action="store_true", help="rotate weight copies past the 256 MB MALL")
     parser.add_argument("--warmup", type=int, default=5)
