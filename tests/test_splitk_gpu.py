@@ -161,7 +161,8 @@ def test_dtype_combinations_with_column_scales(fo, a_dtype, b_dtype, out_dtype):
     bp = fo.prepack_b_for_scaled_mm(_tensor((K, N), b_dtype, seed=1))
     scale = (torch.rand(N, generator=torch.Generator().manual_seed(3)) + 0.5).cuda()
     bias = _tensor((N,), out_dtype, seed=2)
-    for tile in [(2, 2, 4, 4, 4, 1), (2, 2, 4, 4, 8, 1), (2, 4, 4, 4, 4, 1)]:
+    # 128-row tiles and the 64-row ones (deep ring with fp16 activations, shallow with bf16 at M = 200)
+    for tile in [(2, 2, 4, 4, 4, 1), (2, 2, 4, 4, 8, 1), (2, 4, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1), (2, 2, 4, 2, 2, 1)]:
         out = fo.scaled_mm_hip(a, bp, scale, bias, out_dtype, tile=tile, splits=4)
         check_against_oracle(out, a, bp, scale, bias)
 
