@@ -48,6 +48,18 @@ _RING_MODEL = (
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
 _SPLIT_MIN_K = 4096
 _SPLIT_MIN_STAGES = 16
+# M > 64 on a small grid: the 16-row streaming tiles read the weight once per 16 rows (from the L2/MALL
+# after the first pass), and their time grows with those bytes over the fraction of the CUs their blocks
+# keep busy in the last round; from this many bytes by that measure the split ring tiles (which read the
+# weight once per 64 or 128 rows) are faster.
+_RING_MIN_REREAD = 216 << 20
+
+
+def _stream_reread(M: int, N: int, K: int) -> float:
+    """Weight bytes the 16 x 64 streaming tile reads (once per 16 rows), over the fraction of the CU
+    slots its blocks fill in their last round."""
+    blocks = _blocks(M, N, _TILE_STREAM_16x64)
+    return -(-M // 16) * N * K * (_CUS * -(-blocks // _CUS)) / blocks
 # 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more (1.5 times that
 # for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on, the 64 x 64 tile below, split to
 # about _MID_M_RING_BLOCKS workgroups.
@@ -91,9 +103,13 @@ def select_scaled_mm_config(
     - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
       tiles with their measured full-grid rates).
-    - M > 64 with a smaller grid and K >= 4096: the 64 x 128 ring tile (deep ring) up to 256 of its
-      tiles when there are 48 or more 128 x 128 tiles, else the 128 x 128 ring tile (96 tiles or more),
-      split along K (`select_scaled_mm_splits`).
+    - M > 64 with a smaller grid and K >= 4096, once the 16-row streaming tile would read 216 MiB of
+      weight or more (N * K bytes once per 16 rows, over the fraction of CU slots its blocks fill in their
+      last round): the 64 x 128 ring tile (deep ring) up to 256 of its tiles, else the 128 x 128 ring
+      tile (96 tiles or more), split along K (`select_scaled_mm_splits`). Below that the streaming tiles'
+      re-reads hit the caches and they win: 192 x 4096 x 4096 (768 blocks, 201 MB) streams at 461
+      TFLOP/s against 407 for the best split ring; 128 x 3072 x 8192 (384 blocks, 268 MB by the measure)
+      runs 363 on the ring against 323 streaming.
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
     - 16 < M <= 64 with a big weight: the 64-row ring tiles, which read the weight once where the 16-row
       streaming tiles read it once per 16 rows (on small grids they run their deep-ring variant): from a
@@ -113,9 +129,10 @@ def select_scaled_mm_config(
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
         return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
-    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 48 and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
+    ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= _RING_MIN_REREAD
+    if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
         return _TILE_RING_64x128
-    if M > 64 and K >= _SPLIT_MIN_K and tiles_128 >= 96:
+    if ring_split and tiles_128 >= 96:
         return _TILE_RING_128x128
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
@@ -144,8 +161,10 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
 
     Three split regimes of `select_scaled_mm_config`:
     - M > 64, K >= 4096, fewer 128 x 128 tiles than CUs: its 128 x 128 or 64 x 128 ring tile splits into
-      enough K ranges for about 512 workgroups (two per CU), 2 to 8 of them, each at least 16 stages of
-      64 deep. Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
+      2 to 8 K ranges of at least 16 stages of 64 deep, for at most 512 workgroups (two per CU): the
+      count whose workgroups fill the largest fraction of the CUs in their last round, the larger count
+      on a tie (80 tiles: 3 splits, 240 workgroups, 371 TFLOP/s at 128 x 5120 x 5120 against 323 for 4
+      and 330 for 6). Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
     - K >= 8192 with fewer than 192 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
       projection): that tile splits into about 192 workgroups (at most 128 tiles; 2 to 8 splits, each at
       least 2048 deep), or 3 ways from 129 tiles on, so the blocks come close to whole multiples of the
@@ -178,8 +197,14 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if tiles_128 >= _CUS:
         return 1
-    stages = -(-K // 64)
-    return max(2, min(8, (2 * _CUS) // _blocks(M, N, tile), stages // _SPLIT_MIN_STAGES))
+    tiles = _blocks(M, N, tile)
+    most = max(2, min(8, (2 * _CUS) // tiles, -(-K // 64) // _SPLIT_MIN_STAGES))
+
+    def busy(splits: int) -> float:
+        # Fraction of the CU slots the workgroups fill in their last round (one or two per CU).
+        return tiles * splits / (_CUS * -(-tiles * splits // _CUS))
+
+    return max(range(2, most + 1), key=lambda splits: (busy(splits), splits))
 
 
 @functools.lru_cache(maxsize=4096)

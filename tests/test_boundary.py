@@ -209,6 +209,11 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
     assert auto(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)    # short K: no split
     assert auto(192, 1536, 6144) == ((4, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
+    # 64 < M <= 192: streaming below a 24 MiB weight, the split 64 x 128 ring tile from there on
+    assert auto(192, 4096, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 16 MiB, 64 tiles of 128 x 128
+    assert auto(128, 4096, 14336) == ((1, 4, 4, 4, 2, 1), 8)    # 56 MiB, 32 tiles: 64 tiles x 8 = 512
+    assert auto(128, 5120, 5120) == ((1, 4, 4, 4, 2, 1), 3)     # 80 tiles: 240 workgroups, not 400
+    assert auto(256, 4096, 4096) == ((1, 4, 4, 4, 2, 1), 4)     # M > 192: the ring whatever the weight
     assert auto(4096, 12288, 3072) == ((2, 2, 4, 4, 8, 1), 1)   # full grids never split
     assert auto(16, 14336, 4096)[1] == 1
     # skinny M, long K, fewer than 192 16 x 64 streaming tiles: that tile, split for about 192 workgroups

@@ -173,6 +173,8 @@ HEURISTIC_CELLS = [
     (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit
     (1, 96768, 2688),    # 64 x 128 ring tile at one row, an LM-head width (756 tiles)
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
+    (128, 4096, 14336),  # 64 x 128 ring tile split 8 ways (56 MiB weight, 32 tiles of 128 x 128)
+    (128, 5120, 5120),   # 64 x 128 ring tile split 3 ways (80 tiles -> 240 workgroups)
     (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
     (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways
     (2304, 1280, 1280),  # 64 x 64 ring tile
