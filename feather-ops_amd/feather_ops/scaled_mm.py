@@ -53,13 +53,11 @@ _SPLIT_MIN_STAGES = 16
 # keep busy in the last round; from this many bytes by that measure the split ring tiles (which read the
 # weight once per 64 or 128 rows) are faster.
 _RING_MIN_REREAD = 216 << 20
+# M > 768 with a weight too small for the rules above (a few MB, which the streaming tiles re-read from the
+# L2 once per 16 rows): the 64 x 64 ring tile, split along K when that fills more CU slots, wins once its
+# workgroups fill this fraction of the CU slots in their last round.
+_BIG_M_RING_MIN_BUSY = 0.75
 
-
-def _stream_reread(M: int, N: int, K: int) -> float:
-    """Weight bytes the 16 x 64 streaming tile reads (once per 16 rows), over the fraction of the CU
-    slots its blocks fill in their last round."""
-    blocks = _blocks(M, N, _TILE_STREAM_16x64)
-    return -(-M // 16) * N * K * (_CUS * -(-blocks // _CUS)) / blocks
 # 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more (1.5 times that
 # for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on, the 64 x 64 tile below, split to
 # about _MID_M_RING_BLOCKS workgroups.
@@ -79,6 +77,13 @@ _STREAM_SPLIT_MIN_RANGE = 2048
 def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
     bm, bn, _ = gemm_block_sizes(tile)
     return -(-M // bm) * -(-N // bn)
+
+
+def _stream_reread(M: int, N: int, K: int) -> float:
+    """Weight bytes the 16 x 64 streaming tile reads (once per 16 rows), over the fraction of the CU
+    slots its blocks fill in their last round."""
+    blocks = _blocks(M, N, _TILE_STREAM_16x64)
+    return -(-M // 16) * N * K * (_CUS * -(-blocks // _CUS)) / blocks
 
 
 def _ring_time(M: int, N: int, tile: tuple[int, ...], per_cu: int, tflops: float) -> float:
@@ -110,7 +115,9 @@ def select_scaled_mm_config(
       re-reads hit the caches and they win: 192 x 4096 x 4096 (768 blocks, 201 MB) streams at 461
       TFLOP/s against 407 for the best split ring; 128 x 3072 x 8192 (384 blocks, 268 MB by the measure)
       runs 363 on the ring against 323 streaming.
-    - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks, else streaming.
+    - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks; for M > 768 also when it (split
+      along K where that fills more CU slots) fills three quarters of the CU slots in its last round
+      (1024 x 1024 x 3072 split 2 ways: 453 TFLOP/s against 397 streaming); else streaming.
     - 16 < M <= 64 with a big weight: the 64-row ring tiles, which read the weight once where the 16-row
       streaming tiles read it once per 16 rows (on small grids they run their deep-ring variant): from a
       64 MB weight (N * K bytes; 96 MB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
@@ -147,6 +154,8 @@ def select_scaled_mm_config(
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
         return _TILE_STREAM_16x64
+    if M > 768 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
+        return _TILE_RING_64x64
     rows = -(-M // 16)
     for repeat_n in (4, 2, 1):
         if rows * (N // (16 * repeat_n)) >= 160:
@@ -165,6 +174,9 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
       count whose workgroups fill the largest fraction of the CUs in their last round, the larger count
       on a tie (80 tiles: 3 splits, 240 workgroups, 371 TFLOP/s at 128 x 5120 x 5120 against 323 for 4
       and 330 for 6). Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
+    - M > 768 on the 64 x 64 ring tile with fewer than 512 tiles: the same rule (at least one split).
+      1000 x 1000 x 2560 and 1024 x 1024 x 3072 (256 tiles): 2 splits, 394 and 453 TFLOP/s against 329
+      and 358 unsplit.
     - K >= 8192 with fewer than 192 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
       projection): that tile splits into about 192 workgroups (at most 128 tiles; 2 to 8 splits, each at
       least 2048 deep), or 3 ways from 129 tiles on, so the blocks come close to whole multiples of the
@@ -190,6 +202,8 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
             return 1
         aim = round(_STREAM_SPLIT_BLOCKS / tiles) if tiles <= _CUS // 2 else 3
         return max(2, min(8, aim, K // _STREAM_SPLIT_MIN_RANGE))
+    if tile == _TILE_RING_64x64 and M > 768:
+        return _ring_splits(M, N, K, tile)[0] if tile == select_scaled_mm_config(M, N, K) else 1
     if M <= 64 or K < _SPLIT_MIN_K or tile not in (_TILE_RING_128x128, _TILE_RING_64x128):
         return 1
     if tile != select_scaled_mm_config(M, N, K):
@@ -197,14 +211,21 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if tiles_128 >= _CUS:
         return 1
+    return _ring_splits(M, N, K, tile, least=2)[0]
+
+
+def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1) -> tuple[int, float]:
+    """(splits, fraction of the CU slots its workgroups fill in their last round) for a ring tile on a
+    small grid: of `least` to 8 splits of at least 16 stages each and at most 512 workgroups (two per
+    CU), the count that fills the most slots, the larger count on a tie."""
     tiles = _blocks(M, N, tile)
-    most = max(2, min(8, (2 * _CUS) // tiles, -(-K // 64) // _SPLIT_MIN_STAGES))
+    most = max(least, min(8, (2 * _CUS) // tiles, -(-K // 64) // _SPLIT_MIN_STAGES))
 
     def busy(splits: int) -> float:
-        # Fraction of the CU slots the workgroups fill in their last round (one or two per CU).
         return tiles * splits / (_CUS * -(-tiles * splits // _CUS))
 
-    return max(range(2, most + 1), key=lambda splits: (busy(splits), splits))
+    splits = max(range(least, most + 1), key=lambda s: (busy(s), s))
+    return splits, busy(splits)
 
 
 @functools.lru_cache(maxsize=4096)

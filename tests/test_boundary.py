@@ -207,7 +207,11 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(256, 12288, 4096) == ((2, 2, 4, 4, 4, 1), 2)    # 192 tiles
     assert auto(1040, 1024, 5120) == ((1, 4, 4, 4, 2, 1), 3)    # 72 tiles of 128 x 128: 64 x 128, 136 tiles
     assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
-    assert auto(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)    # short K: no split
+    # M > 768, a weight of a few MB: the 64 x 64 ring tile once it fills 3/4 of the CU slots
+    assert auto(1000, 1000, 2560) == ((2, 2, 4, 2, 2, 1), 2)    # 256 tiles -> 512 workgroups
+    assert auto(1536, 1024, 1536) == ((2, 2, 4, 2, 2, 1), 1)    # 384 tiles, 24 stages: unsplit
+    assert auto(1024, 1280, 1280) == ((4, 1, 4, 1, 4, 0), 1)    # 320 tiles fill 5/8: streaming
+    assert auto(768, 1024, 2048) == ((4, 1, 4, 1, 4, 0), 1)     # M <= 768: streaming
     assert auto(192, 1536, 6144) == ((4, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
     # 64 < M <= 192: streaming below a 24 MiB weight, the split 64 x 128 ring tile from there on
     assert auto(192, 4096, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 16 MiB, 64 tiles of 128 x 128

@@ -178,6 +178,7 @@ HEURISTIC_CELLS = [
     (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
     (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways
     (2304, 1280, 1280),  # 64 x 64 ring tile
+    (1000, 1000, 2560),  # 64 x 64 ring tile split 2 ways (M > 768, 256 tiles, ragged M and N)
     (4112, 1024, 5120),  # 64 x 128 ring tile, one partial wave
     (512, 1024, 1024),   # 4-slice streaming tile
     (9216, 2048, 2048),  # 128 x 128 (one full wave of blocks)
