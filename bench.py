@@ -198,7 +198,7 @@ def time_split_cell(m: int, k: int, n: int, unsplit_tile, copies: int = 1, steps
 
     a, bs, s = make_device_inputs(m, k, n, "fp16", copies=copies)
     tile = tuple(feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16))
-    splits = select_scaled_mm_splits(m, n, k, tile)
+    splits = select_scaled_mm_splits(m, n, k, tile, a.dtype)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
     ws = torch.zeros(max(split_workspace_bytes(m, n, k, tile, splits), 1), dtype=torch.uint8, device="cuda")
     nbytes = 2 * m * k + -(-k // 128) * 128 * n + 2 * m * n + 4

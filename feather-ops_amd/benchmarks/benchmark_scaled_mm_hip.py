@@ -98,7 +98,7 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     op = torch.ops.feather_ops.scaled_mm.default
 
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, fp8, out_dtype))
-    picked_splits = select_scaled_mm_splits(m, n, k, picked)
+    picked_splits = select_scaled_mm_splits(m, n, k, picked, a_dtype)
     split_cases = [(tile, splits) for tile in tiles for splits in args.splits
                    if (_blocks(m, n, tile) < _CUS or args.split_any_grid) and _blocks(m, n, tile) * splits <= 4 * _CUS
                    and split_workspace_bytes(m, n, k, tile, splits) > 0]

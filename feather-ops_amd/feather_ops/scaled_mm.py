@@ -53,6 +53,10 @@ _SPLIT_MIN_STAGES = 16
 # keep busy in the last round; from this many bytes by that measure the split ring tiles (which read the
 # weight once per 64 or 128 rows) are faster.
 _RING_MIN_REREAD = 216 << 20
+# With bf16 activations the ring tiles on small grids (M > 64) widen them in registers on the shallow ring
+# and need 4/3 of the re-reads to win; their 64 x 128 tile, light on LDS, then splits for up to three
+# workgroups per CU.
+_BF16_RING_MIN_REREAD = 288 << 20
 # M > 768 with a weight too small for the rules above (a few MB, which the streaming tiles re-read from the
 # L2 once per 16 rows): the 64 x 64 ring tile, split along K when that fills more CU slots, wins once its
 # workgroups fill this fraction of the CU slots in their last round.
@@ -114,10 +118,12 @@ def select_scaled_mm_config(
       tile (96 tiles or more), split along K (`select_scaled_mm_splits`). Below that the streaming tiles'
       re-reads hit the caches and they win: 192 x 4096 x 4096 (768 blocks, 201 MB) streams at 461
       TFLOP/s against 407 for the best split ring; 128 x 3072 x 8192 (384 blocks, 268 MB by the measure)
-      runs 363 on the ring against 323 streaming.
+      runs 363 on the ring against 323 streaming. With bf16 activations from 288 MiB (the shallow ring
+      widens them in registers): 128 x 5120 x 5120 streams at 320 TFLOP/s against 295 on the ring.
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks; for M > 768 also when it (split
       along K where that fills more CU slots) fills three quarters of the CU slots in its last round
-      (1024 x 1024 x 3072 split 2 ways: 453 TFLOP/s against 397 streaming); else streaming.
+      (1024 x 1024 x 3072 split 2 ways: 453 TFLOP/s against 397 streaming; with fp16 activations only,
+      bf16 ones stream faster there); else streaming.
     - 16 < M <= 64 with a big weight: the 64-row ring tiles, which read the weight once where the 16-row
       streaming tiles read it once per 16 rows (on small grids they run their deep-ring variant): from a
       64 MB weight (N * K bytes; 96 MB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
@@ -132,11 +138,13 @@ def select_scaled_mm_config(
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
       columns), with 8 K slices per block up to one block per CU, 4 beyond (two blocks share a CU).
     """
-    del a_dtype, b_dtype, out_dtype
+    del b_dtype, out_dtype
+    a_bf16 = a_dtype == torch.bfloat16
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
         return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
-    ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= _RING_MIN_REREAD
+    min_reread = _BF16_RING_MIN_REREAD if a_bf16 else _RING_MIN_REREAD
+    ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
     if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
         return _TILE_RING_64x128
     if ring_split and tiles_128 >= 96:
@@ -154,7 +162,7 @@ def select_scaled_mm_config(
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
         return _TILE_STREAM_16x64
-    if M > 768 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
+    if M > 768 and not a_bf16 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
         return _TILE_RING_64x64
     rows = -(-M // 16)
     for repeat_n in (4, 2, 1):
@@ -164,7 +172,8 @@ def select_scaled_mm_config(
     return (8 if blocks <= _CUS else 4, 1, 4, 1, repeat_n, 0)
 
 
-def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> int:
+def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
+                            a_dtype: torch.dtype = torch.float16) -> int:
     """K splits for a tile `select_scaled_mm_config` picked (1: none). Not in the reference, whose kernel
     has no split-K.
 
@@ -173,7 +182,9 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
       2 to 8 K ranges of at least 16 stages of 64 deep, for at most 512 workgroups (two per CU): the
       count whose workgroups fill the largest fraction of the CUs in their last round, the larger count
       on a tie (80 tiles: 3 splits, 240 workgroups, 371 TFLOP/s at 128 x 5120 x 5120 against 323 for 4
-      and 330 for 6). Measured 5-40% faster than the best unsplit tile on the grid's cells in that regime.
+      and 330 for 6). With bf16 activations the 64 x 128 tile takes up to three workgroups per CU (768):
+      1040 x 1536 x 6144 584 TFLOP/s split 3 ways against 532 for 2. Measured 5-40% faster than the best
+      unsplit tile on the grid's cells in that regime.
     - M > 768 on the 64 x 64 ring tile with fewer than 512 tiles: the same rule (at least one split).
       1000 x 1000 x 2560 and 1024 x 1024 x 3072 (256 tiles): 2 splits, 394 and 453 TFLOP/s against 329
       and 358 unsplit.
@@ -192,34 +203,36 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...]) -> in
     """
     tile = tuple(tile)
     if tile in (_TILE_RING_64x128, _TILE_RING_64x64) and 16 < M <= 64:
-        if tile != select_scaled_mm_config(M, N, K):
+        if tile != select_scaled_mm_config(M, N, K, a_dtype):
             return 1
         aim = round(_MID_M_RING_BLOCKS / _blocks(M, N, tile))
         return max(1, min(8, aim, -(-K // 64) // _SPLIT_MIN_STAGES))
     if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
         tiles = _blocks(M, N, tile)
-        if tile != select_scaled_mm_config(M, N, K) or tiles >= _STREAM_SPLIT_MAX_TILES:
+        if tile != select_scaled_mm_config(M, N, K, a_dtype) or tiles >= _STREAM_SPLIT_MAX_TILES:
             return 1
         aim = round(_STREAM_SPLIT_BLOCKS / tiles) if tiles <= _CUS // 2 else 3
         return max(2, min(8, aim, K // _STREAM_SPLIT_MIN_RANGE))
     if tile == _TILE_RING_64x64 and M > 768:
-        return _ring_splits(M, N, K, tile)[0] if tile == select_scaled_mm_config(M, N, K) else 1
+        return _ring_splits(M, N, K, tile)[0] if tile == select_scaled_mm_config(M, N, K, a_dtype) else 1
     if M <= 64 or K < _SPLIT_MIN_K or tile not in (_TILE_RING_128x128, _TILE_RING_64x128):
         return 1
-    if tile != select_scaled_mm_config(M, N, K):
+    if tile != select_scaled_mm_config(M, N, K, a_dtype):
         return 1
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if tiles_128 >= _CUS:
         return 1
-    return _ring_splits(M, N, K, tile, least=2)[0]
+    wide_bf16 = a_dtype == torch.bfloat16 and tile == _TILE_RING_64x128
+    return _ring_splits(M, N, K, tile, least=2, per_cu=3 if wide_bf16 else 2)[0]
 
 
-def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1) -> tuple[int, float]:
+def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1,
+                 per_cu: int = 2) -> tuple[int, float]:
     """(splits, fraction of the CU slots its workgroups fill in their last round) for a ring tile on a
-    small grid: of `least` to 8 splits of at least 16 stages each and at most 512 workgroups (two per
-    CU), the count that fills the most slots, the larger count on a tie."""
+    small grid: of `least` to 8 splits of at least 16 stages each and at most `per_cu` workgroups per CU,
+    the count that fills the most slots, the larger count on a tie."""
     tiles = _blocks(M, N, tile)
-    most = max(least, min(8, (2 * _CUS) // tiles, -(-K // 64) // _SPLIT_MIN_STAGES))
+    most = max(least, min(8, (per_cu * _CUS) // tiles, -(-K // 64) // _SPLIT_MIN_STAGES))
 
     def busy(splits: int) -> float:
         return tiles * splits / (_CUS * -(-tiles * splits // _CUS))
@@ -229,11 +242,11 @@ def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1) 
 
 
 @functools.lru_cache(maxsize=4096)
-def _auto_choice(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int, int], int]:
+def _auto_choice(M: int, N: int, K: int, a_dtype: torch.dtype) -> tuple[tuple[int, int, int, int, int, int], int]:
     """(tile, splits) the heuristic picks for a shape, memoized: a model runs the same few shapes again
     and again, and the auto path then skips the model arithmetic (1-5 us of Python per call)."""
-    tile = select_scaled_mm_config(M, N, K)
-    return tile, select_scaled_mm_splits(M, N, K, tile)
+    tile = select_scaled_mm_config(M, N, K, a_dtype)
+    return tile, select_scaled_mm_splits(M, N, K, tile, a_dtype)
 
 
 # Split-K workspaces, one per (device, stream): the counter area at their start must be zero before a
@@ -305,7 +318,7 @@ def _scaled_mm_auto(
     out: torch.Tensor,
 ) -> None:
     """The heuristic behind an opaque boundary: `torch.compile` does not specialize on its branches."""
-    _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1]))
+    _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype))
 
 
 def scaled_mm_hip(
@@ -334,7 +347,7 @@ def scaled_mm_hip(
         if torch.compiler.is_compiling():
             _scaled_mm_auto(a, b_prepacked, scale, bias, out)
         else:
-            _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1]))
+            _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype))
     else:
         if tile is None:
             tile = select_scaled_mm_config(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype,

@@ -217,7 +217,20 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(192, 4096, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 16 MiB, 64 tiles of 128 x 128
     assert auto(128, 4096, 14336) == ((1, 4, 4, 4, 2, 1), 8)    # 56 MiB, 32 tiles: 64 tiles x 8 = 512
     assert auto(128, 5120, 5120) == ((1, 4, 4, 4, 2, 1), 3)     # 80 tiles: 240 workgroups, not 400
-    assert auto(256, 4096, 4096) == ((1, 4, 4, 4, 2, 1), 4)     # M > 192: the ring whatever the weight
+    assert auto(256, 4096, 4096) == ((1, 4, 4, 4, 2, 1), 4)     # 256 MiB of re-reads: the ring
+    # bf16 activations: the ring from 288 MiB of re-reads, the 64 x 128 tile split for up to 768 workgroups,
+    # and no 64 x 64 ring for M > 768 with a small weight
+    bf = torch.bfloat16
+
+    def auto_bf16(m, n, k):
+        tile = pick(m, n, k, bf)
+        return tile, splits(m, n, k, tile, bf)
+
+    assert auto_bf16(256, 4096, 4096) == ((4, 1, 4, 1, 4, 0), 1)
+    assert auto_bf16(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)   # 320 MiB; 80 stages: at most 5 splits
+    assert auto_bf16(1040, 1536, 6144) == ((1, 4, 4, 4, 2, 1), 3)  # 204 tiles x 3 = 612
+    assert auto_bf16(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)
+    assert auto(1040, 1536, 6144)[1] == 2                          # fp16: two per CU at most
     assert auto(4096, 12288, 3072) == ((2, 2, 4, 4, 8, 1), 1)   # full grids never split
     assert auto(16, 14336, 4096)[1] == 1
     # skinny M, long K, fewer than 192 16 x 64 streaming tiles: that tile, split for about 192 workgroups
