@@ -186,19 +186,23 @@ HEURISTIC_CELLS = [
 ]
 
 
+@pytest.mark.parametrize("a_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k", HEURISTIC_CELLS)
-def test_heuristic_regimes(fo, m, n, k):
-    from feather_ops.scaled_mm import select_scaled_mm_config
+def test_heuristic_regimes(fo, m, n, k, a_dtype):
+    """The picks depend on the activation dtype (bf16 ones take the small-grid ring tiles later), so each
+    cell runs the auto path with both."""
+    from feather_ops.scaled_mm import select_scaled_mm_config, select_scaled_mm_splits
 
-    a = _tensor((m, k), torch.bfloat16)
+    a = _tensor((m, k), a_dtype)
     bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
     scale = torch.tensor(0.75, device="cuda", dtype=torch.float32)
     bias = _tensor((n,), torch.bfloat16, seed=2)
     out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16)
-    tile = select_scaled_mm_config(m, n, k, torch.bfloat16, torch.float8_e5m2, torch.bfloat16)
+    tile = select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, torch.bfloat16)
+    splits = select_scaled_mm_splits(m, n, k, tile, a_dtype)
     rows = None if m * n * k <= (1 << 28) else sample_rows(m, n_random=16)
     res = check_against_oracle(out, a, bp, scale, bias, rows=rows)
-    print(f"{m}x{n}x{k} tile {tile}: max_abs={res['max_abs']:.4g} bound={res['bound']:.4g}")
+    print(f"{m}x{n}x{k} tile {tile}/{splits}: max_abs={res['max_abs']:.4g} bound={res['bound']:.4g}")
 
 
 # ---- BASELINE configurations (north-star recipe) -----------------------------------------------------------
