@@ -69,11 +69,11 @@ _MID_M_RING_MIN_WEIGHT = 1 << 26
 _MID_M_WIDE_TILES = 320
 _MID_M_RING_BLOCKS = 512
 
-# The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (from
-# about 200 on, each CU's block already streams enough), aiming at _STREAM_SPLIT_BLOCKS workgroups with at
-# least _STREAM_SPLIT_MIN_RANGE of K each.
+# The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (the
+# 3 splits of more than 128 tiles fit two workgroups per CU up to 170 tiles; at 176 the unsplit tile wins),
+# aiming at _STREAM_SPLIT_BLOCKS workgroups with at least _STREAM_SPLIT_MIN_RANGE of K each.
 _STREAM_SPLIT_MIN_K = 8192
-_STREAM_SPLIT_MAX_TILES = 192
+_STREAM_SPLIT_MAX_TILES = 171
 _STREAM_SPLIT_BLOCKS = 192
 _STREAM_SPLIT_MIN_RANGE = 2048
 
@@ -133,7 +133,7 @@ def select_scaled_mm_config(
       whose direct-to-LDS weight stream runs 5-12% faster than the streaming tiles there; beyond 1024
       tiles the second, partial wave of blocks makes it slower.
     - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
-    - K >= 8192 with fewer than 192 16 x 64 streaming tiles: that tile (8 K slices per block), split along
+    - K >= 8192 with at most 170 16 x 64 streaming tiles: that tile (8 K slices per block), split along
       K across workgroups (`select_scaled_mm_splits`).
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
       columns), with 8 K slices per block up to one block per CU, 4 beyond (two blocks share a CU).
@@ -188,10 +188,11 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
     - M > 768 on the 64 x 64 ring tile with fewer than 512 tiles: the same rule (at least one split).
       1000 x 1000 x 2560 and 1024 x 1024 x 3072 (256 tiles): 2 splits, 394 and 453 TFLOP/s against 329
       and 358 unsplit.
-    - K >= 8192 with fewer than 192 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
+    - K >= 8192 with at most 170 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
       projection): that tile splits into about 192 workgroups (at most 128 tiles; 2 to 8 splits, each at
-      least 2048 deep), or 3 ways from 129 tiles on, so the blocks come close to whole multiples of the
-      CU count. Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
+      least 2048 deep), or 3 ways from 129 to 170 tiles, so the blocks come close to whole multiples of
+      the CU count without passing two per CU (16 x 11264 x 11264, 176 tiles: 160 TFLOP/s unsplit
+      against 132 split 3 ways). Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
       twelve such cells, within 4% of the best split count on most; at 224 tiles (16 x 14336 x 16384) the
       unsplit tile is faster.
     - 16 < M <= 64 on a 64-row ring tile: about 512 workgroups, 1 to 8 splits of at least 16 stages. At

@@ -241,6 +241,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(16, 2048, 8192) == ((8, 1, 4, 1, 4, 0), 4)      # 32 tiles, but K ranges of 2048 at least
     assert auto(1, 512, 65536) == ((8, 1, 4, 1, 4, 0), 8)       # at most 8
     assert auto(16, 14336, 16384) == ((8, 1, 4, 1, 4, 0), 1)    # 224 tiles: unsplit
+    assert auto(16, 11264, 11264) == ((8, 1, 4, 1, 4, 0), 1)    # 176 tiles: 3 splits would pass 2 per CU
     assert auto(8, 28672, 8192) == ((4, 1, 4, 1, 4, 0), 1)      # 448 tiles: a full grid, 4 slices, unsplit
     assert auto(16, 4096, 6144) == ((8, 1, 4, 1, 1, 0), 1)      # K < 8192: narrower tiles instead
     assert auto(32, 25600, 2048) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
