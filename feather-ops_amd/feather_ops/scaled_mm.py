@@ -206,8 +206,13 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
     if tile in (_TILE_RING_64x128, _TILE_RING_64x64) and 16 < M <= 64:
         if tile != select_scaled_mm_config(M, N, K, a_dtype):
             return 1
-        aim = round(_MID_M_RING_BLOCKS / _blocks(M, N, tile))
-        return max(1, min(8, aim, -(-K // 64) // _SPLIT_MIN_STAGES))
+        tiles = _blocks(M, N, tile)
+        splits = max(1, min(8, round(_MID_M_RING_BLOCKS / tiles), -(-K // 64) // _SPLIT_MIN_STAGES))
+        # A last round of workgroups that fills under a quarter of the CUs costs a whole round: one split less
+        # (40 x 8448 x 10496, 132 tiles: 3 splits 270 TFLOP/s, 4 splits = 528 workgroups 228).
+        if splits > 1 and 0 < (tiles * splits) % _CUS < _CUS // 4:
+            splits -= 1
+        return splits
     if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
         tiles = _blocks(M, N, tile)
         if tile != select_scaled_mm_config(M, N, K, a_dtype) or tiles >= _STREAM_SPLIT_MAX_TILES:

@@ -258,6 +258,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(32, 32768, 4096) == ((2, 2, 4, 2, 2, 1), 1)     # 512 tiles of 64 x 64
     assert auto(32, 5120, 25600) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
     assert auto(32, 16384, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 256 32-row tiles: the 16-row tile
+    assert auto(40, 8448, 10496) == ((2, 2, 4, 2, 2, 1), 3)     # 132 tiles: 4 splits would leave 16 over
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
     assert splits(16, 14336, 16384, (8, 1, 4, 1, 4, 0)) == 1    # 224 tiles
