@@ -1,17 +1,22 @@
 """Benchmark of the fp16/bf16 x fp8e5m2 scaled matmul on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rounds R] [--no-cpu] [--no-secondary]
 
 Headline workload (BASELINE.json metric): C3, the DiT MLP up-projection, A fp16 [4096, 3072] x W e5m2
 [12288, 3072] (prepacked [192, 12288, 16], per-tensor scale) -> fp16 [4096, 12288]. One step is one
-`scaled_mm_hip` call on inputs already resident in HBM; K steps are timed with HIP events on the stream
-the kernels run on, bracketed by device synchronisation. value = TFLOP/s = 2*M*N*K / time per step.
+`feather_ops::scaled_mm` launch on inputs already resident in HBM. Timing protocol, for every cell: W
+untimed launches, then rounds of K launches until the clocks settle (at least 1 s of continuous work and
+the last three rounds within 2% of each other, at most 6 s), then R timed rounds of K launches, each
+bracketed by device synchronisation and timed with HIP events on the stream the kernels run on. The
+median round gives ms_per_step; p20 and p80 are reported beside it. value = TFLOP/s = 2*M*N*K / median
+time per step.
 
 Also reported: the skinny HBM-bound cell C4 (A fp16 [16, 4096] x W e5m2 [14336, 4096]) as GB/s of
 algorithmic bytes, timed over a HIP graph of launches that rotate over 8 distinct weight copies (8 x
-58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2, a split-K
-cell (an underfilled grid, 512 x 5120 x 5376, with the best unsplit tile beside it), and the CPU oracle
-(oracle/scaled_mm_oracle.c, all host cores) on a row sample of C3 as `cpu_baseline`.
+58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2, the C3 shape
+with e4m3fn weights, two split-K cells with the unsplit tile beside each, and `cpu_baseline`: the
+reference's CPU path (naive.py's semantics as torch CPU calls with fp32 accumulation) on C1, the
+CPU configuration, on the host's cores.
 
 Prints one JSON line (the driver's contract) on rank 0.
 """
@@ -70,7 +75,59 @@ def make_device_inputs(m, k, n, a_fmt, copies=1, seed=0, fp8="e5m2"):
     return a, bs, scale.reshape(()).to(torch.float32)
 
 
-def time_c3(steps: int, warmup: int):
+def _percentile(values, q):
+    xs = sorted(values)
+    pos = q * (len(xs) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(xs) - 1)
+    return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+
+def steady_rounds(launch_round, launches: int, rounds: int, warmup: int, min_warm_s: float = 1.0,
+                  max_warm_s: float = 6.0, tol: float = 0.02) -> dict:
+    """Time `launch_round` (enqueues `launches` kernel launches on the current stream) at steady state.
+
+    `warmup` untimed launches' worth of rounds first, then more rounds until the clocks settle (at least
+    min_warm_s of continuous work and the last three round times within `tol` of each other; at most
+    max_warm_s), then `rounds` timed rounds. Each round is bracketed by device synchronisation and timed
+    with HIP events on the launching stream. Returns microseconds per launch: median, p20, p80, plus the
+    warm-up actually run.
+    """
+    import torch
+
+    stream = torch.cuda.current_stream()
+
+    def one() -> float:
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        launch_round()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e3 / launches
+
+    t0 = time.perf_counter()
+    warm = [one() for _ in range(max(1, -(-warmup // launches)))]
+    while True:
+        elapsed = time.perf_counter() - t0
+        if elapsed >= max_warm_s:
+            break
+        if elapsed >= min_warm_s and len(warm) >= 3 and max(warm[-3:]) <= (1 + tol) * min(warm[-3:]):
+            break
+        warm.append(one())
+    warm_s = time.perf_counter() - t0
+    timed = [one() for _ in range(rounds)]
+    return {"us": _percentile(timed, 0.5), "p20_us": _percentile(timed, 0.2), "p80_us": _percentile(timed, 0.8),
+            "rounds": rounds, "launches_per_round": launches, "warmup_launches": len(warm) * launches,
+            "warmup_s": round(warm_s, 2), "last_warmup_us": warm[-1]}
+
+
+def _cell_stats(t: dict, flops: float, nbytes: float) -> dict:
+    return {"us_per_launch": round(t["us"], 3), "p20_us": round(t["p20_us"], 3), "p80_us": round(t["p80_us"], 3),
+            "TFLOPs": round(flops / (t["us"] * 1e-6) / 1e12, 1), "GBps": round(nbytes / (t["us"] * 1e-6) / 1e9, 1)}
+
+
+def time_c3(steps: int, warmup: int, rounds: int):
     import torch
 
     import feather_ops
@@ -81,50 +138,38 @@ def time_c3(steps: int, warmup: int):
     tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, b.dtype, torch.float16)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
     op = torch.ops.feather_ops.scaled_mm.default
-    for _ in range(warmup):
-        feather_ops.scaled_mm_hip(a, b, s, None, torch.float16)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
-        op(a, b, s, None, out, *tile)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = start.elapsed_time(stop) / steps
+
+    def launch_round():
+        for _ in range(steps):
+            op(a, b, s, None, out, *tile)
+
+    t = steady_rounds(launch_round, steps, rounds, warmup)
     flops = 2.0 * m * n * k
-    return {"m": m, "k": k, "n": n, "tile": list(tile), "ms": ms, "wall_s": wall, "tflops": flops / (ms * 1e-3) / 1e12,
+    return {"m": m, "k": k, "n": n, "tile": list(tile), "t": t, "tflops": flops / (t["us"] * 1e-6) / 1e12,
             "bytes": algorithmic_bytes(m, k, n)}
 
 
-def time_e4m3_cell(steps: int = 100, warmup: int = 10):
-    """The C3 shape with e4m3fn weights (the other fp8 format the API takes), timed like C3."""
+def time_square_cell(m: int, k: int, n: int, a_fmt: str, fp8: str, steps: int, warmup: int, rounds: int):
+    """One MFMA-bound cell on the heuristic's tile, back-to-back launches, steady state."""
     import torch
 
     import feather_ops
 
-    m, k, n = 4096, 3072, 12288
-    a, bs, s = make_device_inputs(m, k, n, "fp16", fp8="e4m3fn")
-    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.float16)
-    out = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    a, bs, s = make_device_inputs(m, k, n, a_fmt, fp8=fp8)
+    out_dtype = torch.bfloat16 if a_fmt == "bf16" else torch.float16
+    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, out_dtype)
+    out = torch.empty((m, n), dtype=out_dtype, device="cuda")
     op = torch.ops.feather_ops.scaled_mm.default
-    for _ in range(warmup):
-        op(a, bs[0], s, None, out, *tile)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        op(a, bs[0], s, None, out, *tile)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / steps
-    return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+
+    def launch_round():
+        for _ in range(steps):
+            op(a, bs[0], s, None, out, *tile)
+
+    t = steady_rounds(launch_round, steps, rounds, warmup, min_warm_s=0.5)
+    return {"tile": list(tile), **_cell_stats(t, 2.0 * m * n * k, algorithmic_bytes(m, k, n))}
 
 
-def time_c4(reps: int = 50, copies: int = 8):
+def time_c4(rounds: int, copies: int = 8, replays: int = 10):
     import torch
 
     import feather_ops
@@ -145,51 +190,23 @@ def time_c4(reps: int = 50, copies: int = 8):
     with torch.cuda.graph(graph):
         for i in range(launches):
             op(a, bs[i % copies], s, None, outs[i % copies], *tile)
-    graph.replay()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    us = start.elapsed_time(stop) * 1e3 / (reps * launches)
+
+    def launch_round():
+        for _ in range(replays):
+            graph.replay()
+
+    t = steady_rounds(launch_round, launches * replays, rounds, launches, min_warm_s=0.5)
     nbytes = algorithmic_bytes(m, k, n)
-    return {"m": m, "k": k, "n": n, "tile": list(tile), "us": us, "gbps": nbytes / (us * 1e-6) / 1e9,
+    return {"m": m, "k": k, "n": n, "tile": list(tile), "t": t, "gbps": nbytes / (t["us"] * 1e-6) / 1e9,
             "bytes": nbytes, "weight_copies": copies}
 
 
-def time_c2(steps: int = 100, warmup: int = 10):
-    """C2, the bf16-activation cell (bf16 [4096, 3072] x e5m2 [3072, 3072] -> bf16), TFLOP/s."""
-    import torch
-
-    import feather_ops
-
-    m, k, n = 4096, 3072, 3072
-    a, bs, s = make_device_inputs(m, k, n, "bf16")
-    tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.bfloat16)
-    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    op = torch.ops.feather_ops.scaled_mm.default
-    for _ in range(warmup):
-        op(a, bs[0], s, None, out, *tile)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        op(a, bs[0], s, None, out, *tile)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / steps
-    return {"tile": list(tile), "us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
-
-
-def time_split_cell(m: int, k: int, n: int, unsplit_tile, copies: int = 1, steps: int = 100, warmup: int = 10):
+def time_split_cell(m: int, k: int, n: int, unsplit_tile, rounds: int, copies: int = 1, steps: int = 50,
+                    warmup: int = 10):
     """A split-K cell: the heuristic's pick (split along K) and an unsplit tile on fp16 [m, k] x e5m2 [n, k]
     -> fp16, each launched back to back through the op with one preallocated workspace (so the Python
-    layer's per-call cost is not timed), rotating over `copies` weights. Returns us, TFLOP/s and GB/s of
-    algorithmic bytes for both."""
+    layer's per-call cost is not timed), rotating over `copies` weights. Returns per-launch stats for both."""
     import torch
 
     import feather_ops
@@ -201,27 +218,17 @@ def time_split_cell(m: int, k: int, n: int, unsplit_tile, copies: int = 1, steps
     splits = select_scaled_mm_splits(m, n, k, tile, a.dtype)
     out = torch.empty((m, n), dtype=torch.float16, device="cuda")
     ws = torch.zeros(max(split_workspace_bytes(m, n, k, tile, splits), 1), dtype=torch.uint8, device="cuda")
-    nbytes = 2 * m * k + -(-k // 128) * 128 * n + 2 * m * n + 4
+    nbytes = algorithmic_bytes(m, k, n)
     res = {"tile": list(tile), "splits": splits, "unsplit_tile": list(unsplit_tile)}
     for name, t, sp in (("auto", tile, splits), ("unsplit", tuple(unsplit_tile), 1)):
-        def launch(i, t=t, sp=sp):
-            if sp == 1:
-                torch.ops.feather_ops.scaled_mm.default(a, bs[i % copies], s, None, out, *t)
-            else:
-                torch.ops.feather_ops.scaled_mm_splitk.default(a, bs[i % copies], s, None, out, ws, sp, *t)
-        for i in range(warmup):
-            launch(i)
-        torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(steps):
-            launch(i)
-        stop.record(stream)
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(stop) / steps
-        res[name] = {"us": ms * 1e3, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
-                     "gbps": nbytes / (ms * 1e-3) / 1e9}
+        def launch_round(t=t, sp=sp):
+            for i in range(steps):
+                if sp == 1:
+                    torch.ops.feather_ops.scaled_mm.default(a, bs[i % copies], s, None, out, *t)
+                else:
+                    torch.ops.feather_ops.scaled_mm_splitk.default(a, bs[i % copies], s, None, out, ws, sp, *t)
+        res[name] = _cell_stats(steady_rounds(launch_round, steps, rounds, warmup, min_warm_s=0.5),
+                                2.0 * m * n * k, nbytes)
     return res
 
 
@@ -263,37 +270,53 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     torch.cuda.synchronize()
 
 
-def time_cpu_oracle(budget_s: float = 20.0):
-    """The oracle on host cores over a row sample of the C3 workload (the same device-generated inputs,
-    copied to the host), scaled to TFLOP/s. The oracle is the checker; it is only timed here."""
+def _cpu_model() -> str:
+    try:
+        return next(line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo") if line.startswith("model name"))
+    except (OSError, StopIteration):
+        return "unknown"
+
+
+def time_cpu_baseline(runs: int = 9, c3_runs: int = 5):
+    """The reference's CPU path on C1, the CPU configuration (seed 0): naive.py's
+    semantics as torch CPU calls with fp32 accumulation (`oracle.naive.scaled_mm_torch`: unpack, upcast,
+    fp32 matmul, scale, downcast), on every core of this process's CPU share. One warm-up, then the median
+    of `runs` runs; the C3 shape beside it (median of `c3_runs`). The oracle is only timed here."""
     import numpy as np
     import torch
 
     from oracle import naive as oracle
 
-    m, k, n = 4096, 3072, 12288
-    a, bs, s = make_device_inputs(m, k, n, "fp16")
-    a_bits = a.view(torch.int16).cpu().numpy().view(np.uint16)
-    packed = bs[0].view(torch.uint8).cpu().numpy()
-    scale = float(s.item())
-    del a, bs, s
-    threads = min(16, oracle.cpu_count())
-    rows = 32
-    t0 = time.perf_counter()
-    oracle.scaled_mm(a_bits, oracle.F16, packed, oracle.E5M2, scale, None, oracle.F16,
-                     rows=np.arange(rows), threads=threads)
-    t_probe = time.perf_counter() - t0
-    rows = int(max(32, min(m, rows * budget_s / max(t_probe, 1e-3))))
-    sample = np.linspace(0, m - 1, rows).astype(np.int64)
-    t0 = time.perf_counter()
-    oracle.scaled_mm(a_bits, oracle.F16, packed, oracle.E5M2, scale, None, oracle.F16, rows=sample, threads=threads)
-    t = time.perf_counter() - t0
-    try:
-        model = next(line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo") if line.startswith("model name"))
-    except (OSError, StopIteration):
-        model = "unknown"
-    return {"value": 2.0 * rows * n * k / t / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"C3 rows: {rows} of {m} evenly spaced (x all {n} columns, K={k}), {t:.1f} s on {model}"}
+    share = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    threads = min(share, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else share
+    torch.set_num_threads(threads)
+
+    def timed(m, k, n, reps):
+        a_bits, packed, scale, _ = oracle.make_inputs(m, k, n, oracle.F16, seed=0)
+        a = torch.from_numpy(a_bits.view(np.int16)).view(torch.float16)
+        bp = torch.from_numpy(packed).view(torch.float8_e5m2)
+        s = torch.tensor(scale, dtype=torch.float32)
+        oracle.scaled_mm_torch(a, bp, s, None, torch.float16)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            oracle.scaled_mm_torch(a, bp, s, None, torch.float16)
+            times.append(time.perf_counter() - t0)
+        return _percentile(times, 0.5), _percentile(times, 0.2), _percentile(times, 0.8)
+
+    c1 = timed(256, 1024, 1024, runs)
+    c3 = timed(4096, 3072, 12288, c3_runs) if c3_runs else None
+    flops1 = 2.0 * 256 * 1024 * 1024
+    out = {"value": round(flops1 / c1[0] / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": (f"C1 fp16 [256,1024] x e5m2 [1024,1024] -> fp16, seed 0, whole workload: naive.py semantics "
+                      f"as torch CPU calls (unpack, upcast, fp32 matmul, scale, downcast), median of {runs} runs "
+                      f"after 1 warm-up: {c1[0] * 1e3:.3f} ms (p20 {c1[1] * 1e3:.3f}, p80 {c1[2] * 1e3:.3f}); "
+                      f"{threads} threads, nproc {share}, os.cpu_count {os.cpu_count()}, {_cpu_model()}")}
+    if c3 is not None:
+        out["c3"] = {"ms": round(c3[0] * 1e3, 2), "p20_ms": round(c3[1] * 1e3, 2), "p80_ms": round(c3[2] * 1e3, 2),
+                     "TFLOPs": round(2.0 * 4096 * 3072 * 12288 / c3[0] / 1e12, 4), "runs": c3_runs}
+    return out
 
 
 def main() -> int:
@@ -301,7 +324,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    parser.add_argument("--rounds", type=int, default=7, help="timed rounds of --steps launches (at least 5)")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the C4 (HBM), C2 (bf16), e4m3fn and split-K cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3"],
@@ -323,17 +347,21 @@ def main() -> int:
         run_only(args.only, args.steps, args.warmup, tile)
         print(f"ran {args.only}: {args.warmup} + {args.steps} launches")
         return 0
-    c3 = time_c3(args.steps, args.warmup)
-    c4 = None if args.no_secondary else time_c4()
-    c2 = None if args.no_secondary else time_c2()
+    rounds = max(5, args.rounds)
+    c3 = time_c3(args.steps, args.warmup, rounds)
+    sec = not args.no_secondary
+    c4 = time_c4(rounds) if sec else None
+    c2 = time_square_cell(4096, 3072, 3072, "bf16", "e5m2", 50, 10, rounds) if sec else None
+    e4 = time_square_cell(4096, 3072, 12288, "fp16", "e4m3fn", 20, 10, rounds) if sec else None
     # 168 tiles of 128 x 128 for 256 CUs; the unsplit control is the best unsplit tile of the sweep
-    e4 = None if args.no_secondary else time_e4m3_cell()
-    sk = None if args.no_secondary else time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1))
+    sk = time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1), rounds) if sec else None
     # a decoder's down projection at batch 2: 64 tiles of 16 x 64, 67 MB of weight, 8 rotated copies; the
     # unsplit control is the streaming tile the heuristic picks without split-K (16 x 16, 256 blocks)
-    dk = None if args.no_secondary else time_split_cell(2, 16384, 4096, (8, 1, 4, 1, 1, 0), copies=8)
-    cpu = None if args.no_cpu else time_cpu_oracle()
+    dk = time_split_cell(2, 16384, 4096, (8, 1, 4, 1, 1, 0), rounds, copies=8) if sec else None
+    cpu = None if args.no_cpu else time_cpu_baseline()
 
+    t3 = c3["t"]
+    flops3 = 2.0 * c3["m"] * c3["n"] * c3["k"]
     line = {
         "metric": "TFLOP/s (% fp16 MFMA peak) at 4096x3072x12288; HBM GB/s at M=16",
         "value": round(c3["tflops"], 2),
@@ -341,7 +369,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(c3["ms"], 5),
+        "ms_per_step": round(t3["us"] * 1e-3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -350,37 +378,43 @@ def main() -> int:
         "config": {"workload": "C3 DiT MLP up-projection: fp16 [4096,3072] x e5m2 [12288,3072] -> fp16, scale, no bias",
                    "M": c3["m"], "K": c3["k"], "N": c3["n"], "tile": c3["tile"],
                    "pct_fp16_peak": round(100 * c3["tflops"] / PEAK_FP16_TFLOPS, 2)},
+        "timing": {"rounds": t3["rounds"], "steps_per_round": args.steps, "statistic": "median round",
+                   "p20_ms": round(t3["p20_us"] * 1e-3, 5), "p80_ms": round(t3["p80_us"] * 1e-3, 5),
+                   "p20_TFLOPs": round(flops3 / (t3["p80_us"] * 1e-6) / 1e12, 1),
+                   "p80_TFLOPs": round(flops3 / (t3["p20_us"] * 1e-6) / 1e12, 1),
+                   "warmup_launches": t3["warmup_launches"], "warmup_s": t3["warmup_s"],
+                   "warmup_rule": "W launches, then rounds until >= 1 s of work and the last 3 rounds within 2% "
+                                  "(at most 6 s)"},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(c3["tflops"] / PEAK_FP16_TFLOPS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES.get(("c3", tuple(c3["tile"])))},
     }
     if c4 is not None:
+        t4 = c4["t"]
         line["hbm_cell"] = {"workload": "C4 skinny: fp16 [16,4096] x e5m2 [14336,4096] -> fp16",
-                            "GBps": round(c4["gbps"], 1), "us_per_launch": round(c4["us"], 3),
+                            "GBps": round(c4["gbps"], 1), "us_per_launch": round(t4["us"], 3),
+                            "p20_us": round(t4["p20_us"], 3), "p80_us": round(t4["p80_us"], 3),
                             "frac_hbm_peak": round(c4["gbps"] / PEAK_HBM_GBPS, 4), "tile": c4["tile"],
                             "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"],
+                            "timed_as": f"HIP graph of 32 launches, {t4['launches_per_round'] // 32} replays per round, "
+                                        f"median of {t4['rounds']} rounds (launch gaps included)",
                             "traffic": MEASURED_TRAFFIC_BYTES.get(("c4", tuple(c4["tile"])))}
     if c2 is not None:
         line["bf16_cell"] = {"workload": "C2 DiT attention projection: bf16 [4096,3072] x e5m2 [3072,3072] -> bf16",
-                             "TFLOPs": round(c2["tflops"], 1), "us_per_launch": round(c2["us"], 2),
-                             "frac_fp16_peak": round(c2["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": c2["tile"]}
+                             **c2, "frac_fp16_peak": round(c2["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
     if e4 is not None:
         line["e4m3_cell"] = {"workload": "C3 shape with e4m3fn weights: fp16 [4096,3072] x e4m3fn [12288,3072] -> fp16",
-                             "TFLOPs": round(e4["tflops"], 1), "us_per_launch": round(e4["us"], 2),
-                             "frac_fp16_peak": round(e4["tflops"] / PEAK_FP16_TFLOPS, 4), "tile": e4["tile"]}
+                             **e4, "frac_fp16_peak": round(e4["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
     if sk is not None:
         line["splitk_cell"] = {"workload": "underfilled grid: fp16 [512,5120] x e5m2 [5376,5120] -> fp16",
-                               "tile": sk["tile"], "splits": sk["splits"],
-                               "TFLOPs": round(sk["auto"]["tflops"], 1), "us_per_launch": round(sk["auto"]["us"], 2),
-                               "unsplit_64x64_TFLOPs": round(sk["unsplit"]["tflops"], 1)}
+                               "tile": sk["tile"], "splits": sk["splits"], **sk["auto"],
+                               "unsplit_tile": sk["unsplit_tile"], "unsplit": sk["unsplit"]}
     if dk is not None:
         line["decode_split_cell"] = {"workload": "skinny long K: fp16 [2,16384] x e5m2 [4096,16384] -> fp16, "
                                                  "8 rotated weights",
-                                     "tile": dk["tile"], "splits": dk["splits"], "GBps": round(dk["auto"]["gbps"], 1),
-                                     "us_per_launch": round(dk["auto"]["us"], 2),
-                                     "frac_hbm_peak": round(dk["auto"]["gbps"] / PEAK_HBM_GBPS, 4),
-                                     "unsplit_tile": dk["unsplit_tile"],
-                                     "unsplit_GBps": round(dk["unsplit"]["gbps"], 1)}
+                                     "tile": dk["tile"], "splits": dk["splits"], **dk["auto"],
+                                     "frac_hbm_peak": round(dk["auto"]["GBps"] / PEAK_HBM_GBPS, 4),
+                                     "unsplit_tile": dk["unsplit_tile"], "unsplit": dk["unsplit"]}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line))

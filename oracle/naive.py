@@ -25,9 +25,15 @@ What pins each function (tests/test_oracle.py):
   per-output-column scale (`naive.py:29-33`) is pinned by distinct power-of-two column scales (exact:
   column n equals the unscaled column times scale[n], so a row/column mix-up fails), by a constant vector
   agreeing bit for bit with the per-tensor scale, and by float64 loops on tiny inputs.
+- `bf16_to_f16_rtz` (C `oracle_bf16_to_f16_rtz`, the reference's `convert.py:6-21`): all 65,536 bf16
+  codes against torch's fp16 cast where fp16 holds the value exactly (there every rounding mode agrees),
+  +-65504 for every finite code past fp16's range, inf and NaN passed through, and in fp16's subnormal
+  range against the closed form trunc(|x| * 2^24) * 2^-24 with x's sign, evaluated in float64.
 - `scaled_mm_band`: the same core as `scaled_mm` evaluated at the fp32 value -/+ delta; pinned by the
   answer at delta = 0 (itself pinned by the goldens) and by monotonicity (lo <= answer <= hi) on a
   seeded bf16 cell.
+- `scaled_mm_torch` (torch CPU calls, used only as bench.py's timed CPU baseline): against `scaled_mm` on
+  C1's seeded inputs within the north-star bound, and bit for bit on a power-of-two closed form.
 - `literal_fp16_scaled_mm`: the reference's fp16-accumulate form, pinned by the same closed forms; it is
   only used to show the overflow that rules it out as an oracle at BASELINE's quantization.
 """
@@ -97,6 +103,8 @@ def _load():
         for name in ("oracle_f32_to_f16_rne", "oracle_f32_to_bf16_rne"):
             getattr(lib, name).argtypes = [ctypes.c_float]
             getattr(lib, name).restype = ctypes.c_uint16
+        lib.oracle_bf16_to_f16_rtz.argtypes = [ctypes.c_uint16]
+        lib.oracle_bf16_to_f16_rtz.restype = ctypes.c_uint16
         _lib = lib
     return _lib
 
@@ -141,6 +149,14 @@ def widen_bf16_to_f16(bits: np.ndarray) -> np.ndarray:
     flat = np.asarray(bits, dtype=np.uint16).ravel()
     out = [lib.oracle_f32_to_f16_rne(lib.oracle_bf16_to_f32(int(b))) for b in flat]
     return np.array(out, dtype=np.uint16).reshape(np.shape(bits))
+
+
+def bf16_to_f16_rtz(bits: np.ndarray) -> np.ndarray:
+    """bf16 bits -> fp16 bits with round-toward-zero (`convert.py:6-21`, `bf16_to_fp16`): C
+    `oracle_bf16_to_f16_rtz`, evaluated once per distinct code."""
+    lib = _load()
+    table = np.array([lib.oracle_bf16_to_f16_rtz(c) for c in range(65536)], dtype=np.uint16)
+    return table[np.asarray(bits, dtype=np.uint16)]
 
 
 # ---- layout ----------------------------------------------------------------------------------------------
@@ -255,6 +271,28 @@ def scaled_mm_band(a_bits: np.ndarray, a_fmt: str, packed: np.ndarray, b_fmt: st
         None if rws is None else _ptr(rws, ctypes.c_int64), 0 if rws is None else len(rws), int(threads),
     )
     return lo, hi
+
+
+def scaled_mm_torch(a, b_prepacked, scale, bias, out_dtype):
+    """`naive.py:4-41` as torch CPU calls with fp32 accumulation: the reference's CPU path, as timed by
+    bench.py's `cpu_baseline` leg (torch's multi-threaded CPU matmul, not the exact double sum of the C
+    oracle). Takes and returns torch CPU tensors:
+      unpack `permute(0, 2, 1).reshape(kb * 16, N)[:K]` (naive.py:13-16), a.to(fp16), b.to(fp16)
+      (naive.py:20-22), the product in fp32 (naive.py:23, widened), `* scale` in fp32 (naive.py:24-33),
+      `.to(out_dtype)` (naive.py:34), `+ bias` in the output dtype (naive.py:35-40).
+    """
+    import torch
+
+    k = a.shape[1]
+    kb, n, _ = b_prepacked.shape
+    b = b_prepacked.permute(0, 2, 1).reshape(kb * 16, n)[:k]
+    c = a.to(torch.float16).to(torch.float32) @ b.to(torch.float16).to(torch.float32)
+    if scale is not None:
+        c = c * scale.to(torch.float32)
+    c = c.to(out_dtype)
+    if bias is not None:
+        c = c + bias
+    return c
 
 
 def literal_fp16_scaled_mm(a_f16: np.ndarray, b_f16: np.ndarray, scale: float | None) -> np.ndarray:

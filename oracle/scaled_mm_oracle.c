@@ -141,6 +141,38 @@ uint16_t oracle_f32_to_bf16_rne(float f) {
     return (uint16_t)(wide >> 16);
 }
 
+/*
+ * bfloat16 bits -> binary16 bits, rounding toward zero: the semantics of the reference's bf16_to_fp16
+ * (feather_ops/convert.py:6-21, which widens bf16 to fp32 and packs with v_cvt_pkrtz_f16_f32, IEEE
+ * round-toward-zero). Values fp16 holds exactly stay exact; finite values past 65504 truncate to the
+ * largest finite fp16, +-65504, not to inf; inf stays inf and NaN stays (a quiet) NaN; below fp16's normal
+ * range the magnitude truncates to a multiple of 2^-24 (the subnormal quantum), so |x| < 2^-24 becomes a
+ * zero of x's sign. The exponent/mantissa arithmetic below works on the bit fields of the bf16 code.
+ */
+uint16_t oracle_bf16_to_f16_rtz(uint16_t h) {
+    const uint16_t sign = (uint16_t)(h & 0x8000u);
+    const int exp = (h >> 7) & 0xff; /* bf16: 8-bit exponent, bias 127, 7 stored mantissa bits */
+    const uint32_t man = h & 0x7fu;
+    if (exp == 0xff) {
+        return (uint16_t)(sign | (man ? 0x7e00u : 0x7c00u));
+    }
+    if (exp == 0) { /* zero or a bf16 subnormal (< 2^-126): far below fp16's quantum */
+        return sign;
+    }
+    const int e = exp - 127; /* |x| = (1 + man / 128) * 2^e */
+    if (e > 15) {
+        return (uint16_t)(sign | 0x7bffu); /* 65504 */
+    }
+    if (e >= -14) { /* normal in fp16: 10 mantissa bits hold bf16's 7 exactly */
+        return (uint16_t)(sign | (uint16_t)((e + 15) << 10) | (uint16_t)(man << 3));
+    }
+    /* fp16 subnormal: value / 2^-24 = (128 + man) * 2^(e + 24 - 7), truncated */
+    const int shift = e + 24 - 7;
+    const uint32_t sig = 128u + man;
+    const uint32_t q = shift >= 0 ? sig << shift : (shift > -32 ? sig >> -shift : 0u);
+    return (uint16_t)(sign | (uint16_t)q);
+}
+
 static uint16_t finish(float y, const uint16_t* bias, int64_t n, int out_bf16) {
     uint16_t o;
     if (out_bf16) {

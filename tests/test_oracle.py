@@ -83,6 +83,57 @@ def test_bf16_widening_all_codes_match_torch():
     assert np.array_equal(mine[finite], theirs.view(np.uint16)[finite])  # bit-exact incl. signed zeros
 
 
+def test_bf16_to_f16_rtz_all_codes():
+    """The reference's bf16_to_fp16 (round toward zero, convert.py:6-21) on every bf16 code, split by what
+    pins each region: torch's cast where fp16 holds the value exactly (every rounding mode agrees there),
+    saturation to +-65504 past fp16's range, inf/NaN passed through, and the truncation closed form in
+    fp16's subnormal range."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    mine = oracle.bf16_to_f16_rtz(codes)
+    with np.errstate(invalid="ignore"):  # signalling-NaN codes
+        x = (codes.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    mine_f = mine.view(np.float16).astype(np.float64)
+    sign = np.signbit(x)
+    assert np.array_equal(np.signbit(mine_f), sign)  # the sign survives everywhere, zeros and NaNs included
+
+    nan = np.isnan(x)
+    assert np.array_equal(np.isnan(mine_f), nan)
+    inf = np.isinf(x)
+    assert np.array_equal(np.isinf(mine_f), inf)
+
+    finite = ~nan & ~inf
+    big = finite & (np.abs(x) > 65504.0)
+    assert big.sum() > 0 and np.all(np.abs(mine_f[big]) == 65504.0)
+
+    normal = finite & (np.abs(x) >= 2.0**-14) & (np.abs(x) <= 65504.0)
+    torch_f16 = torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16).to(torch.float16)
+    theirs = torch_f16.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(mine[normal], theirs[normal])
+    assert np.array_equal(mine_f[normal], x[normal])  # exact: bf16's 8-bit significand fits fp16's 11
+
+    small = finite & (np.abs(x) < 2.0**-14)
+    want = np.trunc(np.abs(x[small]) * 2.0**24) * 2.0**-24  # multiples of the subnormal quantum, toward 0
+    assert np.array_equal(np.abs(mine_f[small]), want)
+    # the region is not trivial: some codes truncate to a non-zero subnormal, some round down a step that RNE
+    # would round up, and everything under 2^-24 becomes zero
+    assert (want > 0).sum() > 100
+    rne = torch_f16.numpy().astype(np.float64)
+    assert (np.abs(rne[small]) > want).sum() > 50
+    assert np.all(mine_f[finite & (np.abs(x) < 2.0**-24)] == 0.0)
+    assert normal.sum() + small.sum() + big.sum() + nan.sum() + inf.sum() == 65536
+
+
+def test_bf16_to_f16_rtz_catches_a_rounding_mistake():
+    """A planted mistake (round to nearest instead of toward zero) fails the subnormal closed form."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):  # signalling-NaN codes
+        x = (codes.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    small = np.isfinite(x) & (np.abs(x) < 2.0**-14)
+    wrong = torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16).to(torch.float16).numpy()
+    want = np.trunc(np.abs(x[small]) * 2.0**24) * 2.0**-24
+    assert not np.array_equal(np.abs(wrong.astype(np.float64)[small]), want)
+
+
 def _cast_sweep():
     rng = np.random.default_rng(7)
     x = np.concatenate([
@@ -272,6 +323,51 @@ def test_literal_fp16_accumulation_overflows_at_baseline_quantization():
     assert np.isinf(literal).mean() > 0.5
     fp32 = oracle.scaled_mm_f32(a_bits, oracle.F16, packed, oracle.E5M2, scale)
     assert np.isfinite(fp32).all()
+
+
+def _torch_bits(x):
+    return x.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("out_fmt", [oracle.F16, oracle.BF16])
+def test_torch_restatement_matches_the_oracle_on_c1(out_fmt):
+    """The timed CPU baseline (torch CPU calls, fp32 accumulation in torch's matmul order) agrees with the
+    exact-sum oracle on C1's recipe within the north-star bound (bf16: off by one ulp at most, where the bar
+    is below an ulp), with a bias."""
+    a_bits, packed, scale, _ = oracle.make_inputs(256, 1024, 1024, oracle.F16, seed=0)
+    out_dt = torch.bfloat16 if out_fmt == oracle.BF16 else torch.float16
+    bias = torch.randn(1024, generator=torch.Generator().manual_seed(3)).to(out_dt)
+    a = torch.from_numpy(a_bits.view(np.int16)).view(torch.float16)
+    bp = torch.from_numpy(packed).view(torch.float8_e5m2)
+    got = oracle.scaled_mm_torch(a, bp, torch.tensor(scale), bias, out_dt)
+    assert got.dtype == out_dt and got.shape == (256, 1024)
+    ref = oracle.scaled_mm(a_bits, oracle.F16, packed, oracle.E5M2, scale, _torch_bits(bias), out_fmt)
+    res = oracle.compare(_torch_bits(got), ref, out_fmt, 1024)
+    if out_fmt == oracle.F16:
+        assert res["strict_ok"], res
+    else:
+        assert res["nan_ok"] and res["inf_ok"] and res["n_over"] == res["n_over_one_ulp"], res
+
+
+def test_torch_restatement_closed_form():
+    """Small-integer activations and weights (0, +-1, +-2, +-4 as e5m2 codes) and a power-of-two scale: every
+    partial sum is an integer under 2^11, exact in fp32 and in the fp16 output whatever the summation order,
+    so the restatement must give the oracle's bits exactly; a transposed or mis-unpacked weight fails."""
+    k, n, m = 160, 24, 8
+    rng = np.random.default_rng(5)
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float16)
+    values = np.array([0x00, 0x3C, 0x40, 0x44, 0xBC, 0xC0, 0xC4], np.uint8)  # 0, 1, 2, 4, -1, -2, -4
+    codes = values[rng.integers(0, len(values), size=(k, n))]
+    packed = oracle.prepack(codes)
+    got = oracle.scaled_mm_torch(torch.from_numpy(a), torch.from_numpy(packed).view(torch.float8_e5m2),
+                                 torch.tensor(0.5), None, torch.float16)
+    ref = oracle.scaled_mm(a.view(np.uint16), oracle.F16, packed, oracle.E5M2, 0.5, None, oracle.F16)
+    assert np.array_equal(_torch_bits(got), ref)
+    assert np.count_nonzero(ref) > m * n // 2
+    wrong = torch.from_numpy(oracle.prepack(np.ascontiguousarray(codes[::-1])))  # k order reversed
+    bad = oracle.scaled_mm_torch(torch.from_numpy(a), wrong.view(torch.float8_e5m2), torch.tensor(0.5), None,
+                                 torch.float16)
+    assert not np.array_equal(_torch_bits(bad), ref)
 
 
 # ---- the matmul: golden fixtures -------------------------------------------------------------------------
