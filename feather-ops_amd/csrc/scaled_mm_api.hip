@@ -5,6 +5,7 @@
 #include "scaled_mm_launch.h"
 
 #include <cstdint>
+#include <mutex>
 
 namespace feather {
 namespace {
@@ -75,6 +76,56 @@ SplitLayout split_layout(int64_t M, int64_t N, int64_t K, int wm, int wn, int u,
     l.ctr_bytes = kSplitCtrBytes;
     l.total_bytes = total;
     return l;
+}
+
+// ---- the allocation-free split-K entry point's scratch -------------------------------------------------------
+
+// Device memory of feather_scaled_mm_splitk_noalloc, in place of a caller's workspace: the same layout (the
+// 64 KiB counter area, then the partial sums), sized for split launches of up to 512 workgroups of a
+// 128 x 128 ring tile (512 x 64 KiB of fp32 partials), the most the split heuristic launches. Every GPU the
+// library runs on holds its own copy until the process ends. Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address); it uses the address
+// hipGetSymbolAddress returns for the current device.
+constexpr int64_t kScratchBytes = kSplitCtrBytes + (int64_t{32} << 20);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices];   // per device, from hipGetSymbolAddress
+bool g_counters_cleared[kMaxDevices];  // the counter area has been cleared by a kernel that ran eagerly
+
+// Zeroes the counter area with vector stores (a kernel rather than a memset, so that a launch recorded under
+// graph capture replays correctly).
+__global__ __launch_bounds__(256) void clear_counters_kernel(u32x4* ctr, int n16) {
+    const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n16) ctr[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// The current device's scratch, set up on the first call on that device (and until a clear has run outside
+// graph capture, each call enqueues one on `stream` ahead of the kernel: a clear recorded into a graph only
+// runs when the graph does). nullptr if the device or the symbol lookup fails.
+uint8_t* device_scratch(hipStream_t stream) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+    }
+    if (!g_counters_cleared[dev]) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &capture) != hipSuccess) return nullptr;
+        u32x4* ctr = reinterpret_cast<u32x4*>(g_scratch_ptr[dev]);
+        int n16 = static_cast<int>(kSplitCtrBytes / 16);
+        void* args[] = {&ctr, &n16};
+        if (hipLaunchKernel(reinterpret_cast<const void*>(clear_counters_kernel), dim3((n16 + 255) / 256), dim3(256),
+                            args, 0, stream) != hipSuccess) {
+            return nullptr;
+        }
+        g_counters_cleared[dev] = capture == hipStreamCaptureStatusNone;
+    }
+    return g_scratch_ptr[dev];
 }
 
 bool launch(const Params& p, bool use_fp8_e5m2, bool a_bf16, bool output_bf16, const TileQuery& t,
@@ -153,6 +204,31 @@ extern "C" bool feather_scaled_mm_splitk(const uint16_t* const a, const uint8_t*
         p.splits = splits;
         p.split_ctr = static_cast<uint32_t*>(workspace);
         p.split_part = static_cast<uint8_t*>(workspace) + l.ctr_bytes;
+    }
+    const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
+    return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);
+}
+
+extern "C" bool feather_scaled_mm_splitk_noalloc(const uint16_t* const a, const uint8_t* const b_prepacked,
+                                                 const float* const scale, const uint16_t* const bias,
+                                                 uint16_t* const c, const int64_t M, const int64_t N, const int64_t K,
+                                                 const int has_scale, const int has_bias, const bool use_fp8_e5m2,
+                                                 const bool a_bf16, const bool output_bf16, const int block_warps_m,
+                                                 const int block_warps_n, const int unroll_k, const int repeat_m,
+                                                 const int repeat_n, const bool prefetch, const int splits,
+                                                 hipStream_t stream) {
+    using namespace feather;
+    if (!contract_ok(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias)) return false;
+    const SplitLayout l =
+        split_layout(M, N, K, block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch, splits);
+    if (l.total_bytes < 0 || l.total_bytes > kScratchBytes) return false;
+    Params p = make_params(a, b_prepacked, scale, bias, c, M, N, K, has_scale, has_bias);
+    if (splits > 1) {
+        uint8_t* const ws = device_scratch(stream);
+        if (!ws) return false;
+        p.splits = splits;
+        p.split_ctr = reinterpret_cast<uint32_t*>(ws);
+        p.split_part = ws + l.ctr_bytes;
     }
     const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
     return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);

@@ -73,6 +73,26 @@ bool feather_scaled_mm_splitk(const uint16_t* a, const uint8_t* b_prepacked, con
                               int splits, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * feather_scaled_mm_splitk without a workspace argument and without any allocation: the partial sums and
+ * arrival counters live in a static device array of the library (64 KiB of counters + 32 MiB of partials on
+ * each GPU it runs on, held until the process ends), so callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) can still split K. It calls
+ * no hipMalloc, hipFree or allocating library routine; its first call on a device looks the array up
+ * (hipGetSymbolAddress) and enqueues a small kernel on `stream` that zeroes the counters.
+ *
+ * No counterpart in the reference. Same arguments, contract and results as feather_scaled_mm_splitk,
+ * minus the workspace. Returns false (nothing enqueued) where that function would, and also when the
+ * launch needs more than the static array holds, i.e. when feather_splitk_workspace_bytes(...) exceeds
+ * 65536 + 33554432 bytes. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams or threads without ordering) race and must not be made.
+ */
+bool feather_scaled_mm_splitk_noalloc(const uint16_t* a, const uint8_t* b_prepacked, const float* scale,
+                                      const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K,
+                                      int has_scale, int has_bias, bool use_fp8_e5m2, bool a_bf16, bool output_bf16,
+                                      int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, int repeat_n,
+                                      bool prefetch, int splits, hipStream_t stream);
+
+/*
  * Workspace bytes feather_scaled_mm_splitk needs for this shape, tile and split count (host only, no GPU
  * call): 0 for splits = 1, -1 if they are outside its contract. Always under 2 GiB.
  */

@@ -38,6 +38,9 @@ def lib():
     handle.feather_scaled_mm_splitk.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + \
         [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_int] + \
         [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    handle.feather_scaled_mm_splitk_noalloc.restype = ctypes.c_bool
+    handle.feather_scaled_mm_splitk_noalloc.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + \
+        [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_int, ctypes.c_void_p]
     handle.feather_splitk_workspace_bytes.restype = ctypes.c_int64
     handle.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 5 + \
         [ctypes.c_bool, ctypes.c_int]
@@ -47,7 +50,8 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     names = _declared()
     assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_prepack_b",
-                          "feather_scaled_mm_splitk", "feather_splitk_workspace_bytes"}
+                          "feather_scaled_mm_splitk", "feather_splitk_workspace_bytes",
+                          "feather_scaled_mm_splitk_noalloc"}
     for name in names:
         assert hasattr(lib, name), name
 
@@ -105,6 +109,25 @@ def _split(lib, tile=(2, 2, 4, 4, 4, True), splits=2, ws=WS, ws_bytes=1 << 30, M
 ])
 def test_splitk_c_abi_refuses_out_of_contract_calls(lib, kwargs):
     assert _split(lib, **kwargs) is False
+
+
+def test_noalloc_splitk_refuses_past_its_static_array_and_out_of_contract(lib):
+    """feather_scaled_mm_splitk_noalloc refuses, before any GPU call, a launch whose workspace would exceed
+    its static array (64 KiB + 32 MiB), and everything feather_scaled_mm_splitk refuses."""
+    scratch = 65536 + (32 << 20)
+    tile = (2, 2, 4, 4, 4, True)
+
+    def call(m, n, k, splits, c=C):
+        return lib.feather_scaled_mm_splitk_noalloc(A, B, S, BIAS, c, m, n, k, 1, 1, True, False, False, *tile,
+                                                    splits, None)
+
+    assert lib.feather_splitk_workspace_bytes(4096, 4096, 2560, *tile, 8) > scratch
+    assert call(4096, 4096, 2560, 8) is False            # 1024 tiles x 8 splits x 64 KiB
+    assert lib.feather_splitk_workspace_bytes(2048, 4096, 2560, *tile, 2) > scratch
+    assert call(2048, 4096, 2560, 2) is False            # 512 tiles x 2 splits: one over
+    assert call(4096, 4096, 2560, 33) is False           # more than 32 splits
+    assert call(64, 100, 256, 2) is False                # N % 8
+    assert call(64, 128, 256, 2, c=C + 2) is False       # misaligned output
 
 
 def test_splitk_workspace_bytes_match_the_python_formula(lib):
