@@ -477,6 +477,58 @@ __device__ __forceinline__ int a_unit_phys(int row, int u) {
     return u ^ a_swizzle_key<kUnits>(row);
 }
 
+// A wave's epilogue staged through LDS, for kernels whose waves all reach it (a block barrier comes first):
+// the wave writes its rounded, biased 16 RM x 16 RN output tile into its own LDS area (`area`, rows
+// 16 RN * 2 + 16 bytes apart, so the 8-byte writes of a fragment's 16 rows fall in distinct banks), then stores
+// it as 16-byte pieces, consecutive lanes covering whole row segments (2 RN lanes per row, 32 / RN rows per
+// instruction). Against the 8-byte stores of 16 rows x 32 bytes that store_wave_tiles issues: half the store
+// instructions, and every row segment written whole (measured 4.8% faster on a 128 x 256 tile).
+template <int RM, int RN, bool kOutBf16>
+__device__ __forceinline__ void store_wave_tiles_via_lds(const Params& p, const f32x4 (&acc)[RM][RN], uint8_t* area,
+                                                         int row0, int col0, int lane, float scale) {
+    constexpr int kRowBytes = 16 * RN * 2;
+    constexpr int kPitch = kRowBytes + 16;
+    constexpr int kRows = 16 * RM;
+    constexpr int kLanesPerRow = kRowBytes / 16;
+    constexpr int kRowsPerInstr = kWave / kLanesPerRow;
+    static_assert(kWave % kLanesPerRow == 0 && kRows % kRowsPerInstr == 0, "whole rows per store instruction");
+    u32x2 bias_bits[RN];
+    load_bias<RN>(p, col0, lane, bias_bits);
+    f32x4 col_scales[RN];
+    if (p.col_scale) load_col_scales<RN>(p, col0, lane, col_scales);
+    const bool has_bias = p.bias != nullptr;
+    const int r_in = lane & 15;
+    const int c_in = 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j) {
+            const f32x4 sc = p.col_scale ? col_scales[j] : f32x4{scale, scale, scale, scale};
+            *reinterpret_cast<u32x2*>(area + (16 * i + r_in) * kPitch + (16 * j + c_in) * 2) =
+                epilogue4<kOutBf16>(acc[i][j], sc, has_bias, bias_bits[j]);
+        }
+    __builtin_amdgcn_s_waitcnt(kLgkm0Imm);  // the wave reads back only what it wrote itself
+    const rsrc_t c_rsrc = make_rsrc(p.c, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.N) * 2u);
+    // N % 8 == 0, so a piece of 8 columns lies wholly inside N or wholly outside
+    const int col = col0 + (lane % kLanesPerRow) * 8;
+#pragma unroll
+    for (int q = 0; q < kRows / kRowsPerInstr; ++q) {
+        const int r = kRowsPerInstr * q + lane / kLanesPerRow;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(area + r * kPitch + (lane % kLanesPerRow) * 16);
+        const int row = row0 + r;
+        const uint32_t off = col < p.N && row < p.M ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.N) +
+                                                       static_cast<uint32_t>(col)) * 2u
+                                                    : kOob;
+        __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(off), 0, 0);
+    }
+}
+
+// LDS bytes store_wave_tiles_via_lds stages per wave.
+template <int RM, int RN>
+constexpr int lds_epilogue_bytes() {
+    return 16 * RM * (16 * RN * 2 + 16);
+}
+
 // kSplitK: this launch splits K (p.splits > 1). A separate instantiation, so the unsplit kernel carries no
 // join code (its partial reads raise register pressure: measured 3% slower on a 128 x 256 tile).
 // kDeep: the deep-ring variant of a 64-row tile (DmaShape), chosen by the launcher for small grids.
@@ -730,9 +782,16 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
     }
 
     if constexpr (kSplitK) {
+        // waves leave after the join unless they are their tile's last: no block barrier, per-wave stores
         if (!join_split<S::kWaves, RM, RN>(p, acc, tile_id, split, wave, lane)) return;
+        store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale);
+    } else {
+        // the ring is free once every wave has read the last stage: stage the output through it
+        static_assert(S::kWaves * lds_epilogue_bytes<RM, RN>() <= S::kLdsBytes, "epilogue staging fits the ring");
+        __syncthreads();
+        store_wave_tiles_via_lds<RM, RN, kOutBf16>(p, acc, lds + wave * lds_epilogue_bytes<RM, RN>(),
+                                                   m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale);
     }
-    store_wave_tiles<RM, RN, kOutBf16>(p, acc, m0 + wave_m * 16 * RM, n0 + wave_n * 16 * RN, lane, scale);
 }
 
 // ---- stream kernel: split-K, global -> VGPR ----------------------------------------------------------------
