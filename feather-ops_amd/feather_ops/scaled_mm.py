@@ -22,7 +22,7 @@ import torch
 from torch.library import custom_op
 
 from . import _lib
-from .tiles import gemm_block_sizes, split_workspace_bytes
+from .tiles import gemm_block_sizes, ring_is_deep, split_workspace_bytes
 
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
 _TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
@@ -62,6 +62,19 @@ _BF16_RING_MIN_REREAD = 288 << 20
 # workgroups fill this fraction of the CU slots in their last round.
 _BIG_M_RING_MIN_BUSY = 0.75
 
+# M > 64 on a small grid with more than 256 64 x 128 tiles: the tile and split count come from a time model of
+# the candidates (the 64 x 128 tile split 1-3 ways, the 128 x 128 tile split 1-4 ways), fitted with the tile sweep
+# on 106 such cells, fp16 and bf16 activations (feather-ops_amd/benchmarks). Per tile: its rate relative to the
+# 128 x 128 tile and how much of a CU's rate 1, 2 and 3+ resident blocks reach; blocks per CU from the compiled
+# kernels (128 x 128: 3, by registers and its 48 KiB ring; 64 x 128: 5 on the 32 KiB shallow ring, 2 on the 56 KiB
+# deep ring); each block also pays a fixed cost worth _SMALL_GRID_BLOCK_K of K (prologue, epilogue, the partial
+# sums' round trip).
+_SMALL_GRID_RATE = {_TILE_RING_64x128: (0.85, (0.4, 0.9, 1.0)), _TILE_RING_128x128: (1.0, (0.5, 0.9, 1.0))}
+_SMALL_GRID_BLOCK_K = 768
+_SMALL_GRID_MAX_SPLITS = {_TILE_RING_64x128: 3, _TILE_RING_128x128: 4}
+# Partial sums of one split launch stay within the allocation-free entry point's static array.
+_SPLIT_MAX_PARTIAL_BYTES = 64 << 20
+
 # 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more (1.5 times that
 # for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on, the 64 x 64 tile below, split to
 # about _MID_M_RING_BLOCKS workgroups.
@@ -90,6 +103,43 @@ def _stream_reread(M: int, N: int, K: int) -> float:
     return -(-M // 16) * N * K * (_CUS * -(-blocks // _CUS)) / blocks
 
 
+def _small_grid_time(M: int, N: int, K: int, tile: tuple[int, ...], splits: int, a_bf16: bool) -> float:
+    """Modelled time of a ring tile split `splits` ways on a small grid (arbitrary units): the busiest CU
+    runs ceil(workgroups / CUs) workgroups, as many at once as fit, each round at the rate its resident count
+    reaches, plus a fixed cost per workgroup."""
+    bm, bn, _ = gemm_block_sizes(tile)
+    workgroups = _blocks(M, N, tile) * splits
+    if tile == _TILE_RING_128x128:
+        per_cu = 3
+    else:
+        per_cu = 2 if ring_is_deep(M, N, tile, splits, a_bf16) else 5
+    rate, efficiency = _SMALL_GRID_RATE[tile]
+    work = bm * bn * K / splits
+    left = -(-workgroups // _CUS)
+    time = left * bm * bn * _SMALL_GRID_BLOCK_K / rate
+    while left > 0:
+        resident = min(per_cu, left)
+        time += resident * work / (rate * efficiency[min(resident, 3) - 1])
+        left -= resident
+    return time
+
+
+def _small_grid_choice(M: int, N: int, K: int, a_bf16: bool) -> tuple[tuple[int, int, int, int, int, int], int]:
+    """(tile, splits) with the least modelled time among the 64 x 128 and 128 x 128 ring tiles and their
+    split counts (each split at least 16 stages of 64, partial sums within _SPLIT_MAX_PARTIAL_BYTES)."""
+    best = None
+    for tile in (_TILE_RING_64x128, _TILE_RING_128x128):
+        bm, bn, _ = gemm_block_sizes(tile)
+        for splits in range(1, _SMALL_GRID_MAX_SPLITS[tile] + 1):
+            if splits > 1 and (-(-K // 64) // splits < _SPLIT_MIN_STAGES or
+                               _blocks(M, N, tile) * splits * bm * bn * 4 > _SPLIT_MAX_PARTIAL_BYTES):
+                break
+            time = _small_grid_time(M, N, K, tile, splits, a_bf16)
+            if best is None or time < best[0]:
+                best = (time, tile, splits)
+    return best[1], best[2]
+
+
 def _ring_time(M: int, N: int, tile: tuple[int, ...], per_cu: int, tflops: float) -> float:
     """Relative time of a ring tile: whole waves of `_CUS * per_cu` blocks, each wave as long as a full one."""
     bm, bn, _ = gemm_block_sizes(tile)
@@ -108,18 +158,23 @@ def select_scaled_mm_config(
     """Static tile choice for one shape (same signature as the reference's `scaled_mm.py:35-42`).
 
     Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile and split count;
-    with `select_scaled_mm_splits` the pick is within 1.2% of the best candidate in geometric mean):
+    with `select_scaled_mm_splits` the pick is within 0.7% of the best candidate in geometric mean) and
+    extra cells where the grid had few:
     - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
       tiles with their measured full-grid rates).
     - M > 64 with a smaller grid and K >= 4096, once the 16-row streaming tile would read 216 MiB of
       weight or more (N * K bytes once per 16 rows, over the fraction of CU slots its blocks fill in their
-      last round): the 64 x 128 ring tile (deep ring) up to 256 of its tiles, else the 128 x 128 ring
-      tile (96 tiles or more), split along K (`select_scaled_mm_splits`). Below that the streaming tiles'
-      re-reads hit the caches and they win: 192 x 4096 x 4096 (768 blocks, 201 MB) streams at 461
-      TFLOP/s against 407 for the best split ring; 128 x 3072 x 8192 (384 blocks, 268 MB by the measure)
-      runs 363 on the ring against 323 streaming. With bf16 activations from 288 MiB (the shallow ring
-      widens them in registers): 128 x 5120 x 5120 streams at 320 TFLOP/s against 295 on the ring.
+      last round): the 64 x 128 ring tile (deep ring) up to 256 of its tiles, split along K
+      (`select_scaled_mm_splits`); beyond that the 64 x 128 or 128 x 128 ring tile and split count with the
+      least modelled time (`_small_grid_choice`: 0.990 of the best candidate in geometric mean on 58 fp16
+      cells of that regime, 0.994 on 30 held-out ones and 0.994 / 0.983 with bf16 activations, against
+      0.933 / 0.978 / 0.910 / 0.967 for the rule it replaced, which took the 128 x 128 tile split for two
+      workgroups per CU: 448 x 6144 x 8192 runs 814 TFLOP/s on the 64 x 128 tile split 3 ways against 679).
+      Below that the streaming tiles' re-reads hit the caches and they win: 192 x 4096 x 4096 (768 blocks,
+      201 MB) streams at 461 TFLOP/s against 407 for the best split ring; 128 x 3072 x 8192 (384 blocks, 268 MB
+      by the measure) runs 363 on the ring against 323 streaming. With bf16 activations from 288 MiB (the
+      shallow ring widens them in registers): 128 x 5120 x 5120 streams at 320 TFLOP/s against 295 on the ring.
     - M > 64 otherwise: the 64 x 64 ring tile once it gives 512 blocks; for M > 768 also when it (split
       along K where that fills more CU slots) fills three quarters of the CU slots in its last round
       (1024 x 1024 x 3072 split 2 ways: 453 TFLOP/s against 397 streaming; with fp16 activations only,
@@ -147,8 +202,8 @@ def select_scaled_mm_config(
     ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
     if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
         return _TILE_RING_64x128
-    if ring_split and tiles_128 >= 96:
-        return _TILE_RING_128x128
+    if ring_split:
+        return _small_grid_choice(M, N, K, a_bf16)[0]
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
     if 16 < M <= 64 and N * K >= _MID_M_RING_MIN_WEIGHT * (2 if M > 32 else 3) // 2:
@@ -178,13 +233,14 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
     has no split-K.
 
     Three split regimes of `select_scaled_mm_config`:
-    - M > 64, K >= 4096, fewer 128 x 128 tiles than CUs: its 128 x 128 or 64 x 128 ring tile splits into
-      2 to 8 K ranges of at least 16 stages of 64 deep, for at most 512 workgroups (two per CU): the
+    - M > 64, K >= 4096, fewer 128 x 128 tiles than CUs: with at most 256 64 x 128 tiles, that tile splits
+      into 2 to 8 K ranges of at least 16 stages of 64 deep, for at most 512 workgroups (two per CU): the
       count whose workgroups fill the largest fraction of the CUs in their last round, the larger count
       on a tie (80 tiles: 3 splits, 240 workgroups, 371 TFLOP/s at 128 x 5120 x 5120 against 323 for 4
       and 330 for 6). With bf16 activations the 64 x 128 tile takes up to three workgroups per CU (768):
       1040 x 1536 x 6144 584 TFLOP/s split 3 ways against 532 for 2. Measured 5-40% faster than the best
-      unsplit tile on the grid's cells in that regime.
+      unsplit tile on the grid's cells in that regime. With more 64 x 128 tiles, the split count of the
+      model that chose the tile (`_small_grid_choice`, 1 to 4).
     - M > 768 on the 64 x 64 ring tile with fewer than 512 tiles: the same rule (at least one split).
       1000 x 1000 x 2560 and 1024 x 1024 x 3072 (256 tiles): 2 splits, 394 and 453 TFLOP/s against 329
       and 358 unsplit.
@@ -228,6 +284,8 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if tiles_128 >= _CUS:
         return 1
+    if _blocks(M, N, _TILE_RING_64x128) > _CUS:
+        return _small_grid_choice(M, N, K, a_dtype == torch.bfloat16)[1]
     wide_bf16 = a_dtype == torch.bfloat16 and tile == _TILE_RING_64x128
     return _ring_splits(M, N, K, tile, least=2, per_cu=3 if wide_bf16 else 2)[0]
 

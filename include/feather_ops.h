@@ -74,7 +74,7 @@ bool feather_scaled_mm_splitk(const uint16_t* a, const uint8_t* b_prepacked, con
 
 /*
  * feather_scaled_mm_splitk without a workspace argument and without any allocation: the partial sums and
- * arrival counters live in a static device array of the library (64 KiB of counters + 32 MiB of partials on
+ * arrival counters live in a static device array of the library (64 KiB of counters + 64 MiB of partials on
  * each GPU it runs on, held until the process ends), so callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) can still split K. It calls
  * no hipMalloc, hipFree or allocating library routine; its first call on a device looks the array up

@@ -113,8 +113,8 @@ def test_splitk_c_abi_refuses_out_of_contract_calls(lib, kwargs):
 
 def test_noalloc_splitk_refuses_past_its_static_array_and_out_of_contract(lib):
     """feather_scaled_mm_splitk_noalloc refuses, before any GPU call, a launch whose workspace would exceed
-    its static array (64 KiB + 32 MiB), and everything feather_scaled_mm_splitk refuses."""
-    scratch = 65536 + (32 << 20)
+    its static array (64 KiB + 64 MiB), and everything feather_scaled_mm_splitk refuses."""
+    scratch = 65536 + (64 << 20)
     tile = (2, 2, 4, 4, 4, True)
 
     def call(m, n, k, splits, c=C):
@@ -123,8 +123,9 @@ def test_noalloc_splitk_refuses_past_its_static_array_and_out_of_contract(lib):
 
     assert lib.feather_splitk_workspace_bytes(4096, 4096, 2560, *tile, 8) > scratch
     assert call(4096, 4096, 2560, 8) is False            # 1024 tiles x 8 splits x 64 KiB
-    assert lib.feather_splitk_workspace_bytes(2048, 4096, 2560, *tile, 2) > scratch
-    assert call(2048, 4096, 2560, 2) is False            # 512 tiles x 2 splits: one over
+    assert lib.feather_splitk_workspace_bytes(2048, 4096, 2560, *tile, 2) == scratch   # 1024 x 64 KiB: fits
+    assert lib.feather_splitk_workspace_bytes(2048, 4224, 2560, *tile, 2) > scratch
+    assert call(2048, 4224, 2560, 2) is False            # 528 tiles x 2 splits: 32 workgroups over
     assert call(4096, 4096, 2560, 33) is False           # more than 32 splits
     assert call(64, 100, 256, 2) is False                # N % 8
     assert call(64, 128, 256, 2, c=C + 2) is False       # misaligned output
@@ -227,7 +228,11 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
 
     assert auto(512, 5376, 5120) == ((2, 2, 4, 4, 4, 1), 3)     # 168 tiles -> 504 workgroups
     assert auto(1040, 1536, 6144) == ((1, 4, 4, 4, 2, 1), 2)    # 204 tiles of 64 x 128 (deep ring)
-    assert auto(256, 12288, 4096) == ((2, 2, 4, 4, 4, 1), 2)    # 192 tiles
+    # more than 256 64 x 128 tiles: the small-grid time model (measured best or within 5% of it)
+    assert auto(256, 12288, 4096) == ((1, 4, 4, 4, 2, 1), 2)    # 384 tiles of 64 x 128 -> 768 workgroups
+    assert auto(448, 6144, 8192) == ((1, 4, 4, 4, 2, 1), 3)     # 336 tiles -> 1008, the shallow ring
+    assert auto(256, 12288, 8192) == ((2, 2, 4, 4, 4, 1), 4)    # 192 tiles of 128 x 128 -> 768, 3 per CU
+    assert auto(2320, 1536, 6144) == ((2, 2, 4, 4, 4, 1), 2)    # 444 tiles of 64 x 128: 128 x 128 split
     assert auto(1040, 1024, 5120) == ((1, 4, 4, 4, 2, 1), 3)    # 72 tiles of 128 x 128: 64 x 128, 136 tiles
     assert auto(128, 8192, 5120) == ((1, 4, 4, 4, 2, 1), 4)
     # M > 768, a weight of a few MB: the 64 x 64 ring tile once it fills 3/4 of the CU slots

@@ -175,7 +175,9 @@ HEURISTIC_CELLS = [
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
     (128, 4096, 14336),  # 64 x 128 ring tile split 8 ways (56 MiB weight, 32 tiles of 128 x 128)
     (128, 5120, 5120),   # 64 x 128 ring tile split 3 ways (80 tiles -> 240 workgroups)
-    (256, 12288, 4096),  # 128 x 128 ring tile split 2 ways along K
+    (256, 12288, 4096),  # 64 x 128 ring tile split 2 ways (384 tiles: the small-grid time model)
+    (448, 6144, 8192),   # 64 x 128 ring tile split 3 ways, 1008 workgroups on the shallow ring
+    (256, 12288, 8192),  # 128 x 128 ring tile split 4 ways, 768 workgroups (48 MiB of partial sums)
     (1040, 1024, 5120),  # 64 x 128 ring tile split 3 ways
     (2304, 1280, 1280),  # 64 x 64 ring tile
     (1000, 1000, 2560),  # 64 x 64 ring tile split 2 ways (M > 768, 256 tiles, ragged M and N)
