@@ -69,6 +69,9 @@ struct Params {
     int32_t splits;
     uint32_t* split_ctr;        // [tiles * waves] arrival counters: zero before a launch, zero after it
     uint8_t* split_part;        // [tiles][splits][waves][RM * RN][64 lanes] fp32x4 partial sums
+    // Ring kernel: workgroups [0, reads_first_blocks) take the reads-first operand schedule, the rest the
+    // interleaved one (0: all interleaved). The launcher picks it from the grid's CU occupancy.
+    int32_t reads_first_blocks;
 };
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -416,6 +419,12 @@ constexpr int lcm(int a, int b) {
     return a / gcd(a, b) * b;
 }
 
+// A compile-time choice passed to generic lambdas.
+template <bool B>
+struct Flag {
+    static constexpr bool value = B;
+};
+
 template <int WM, int WN, int U, int RM, int RN, bool kDeep = false>
 struct DmaShape {
     static constexpr int kWaves = WM * WN;
@@ -445,8 +454,12 @@ struct DmaShape {
     static constexpr int kPeriod = lcm(kSlotsA, kSlotsB);  // one period of both rings: compile-time slots
     static constexpr int kBRing = kSlotsA * kABytes;  // LDS offset of the B ring
     static constexpr int kLdsBytes = kSlotsA * kABytes + kSlotsB * kBBytes;
-    // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two.
-    static constexpr int kWavesPerEu = (kWaves <= 4 ? 2 : 1) * ((kWaves + 3) / 4);
+    // Blocks per CU the LDS allows (the register budgets of the tiles allow as many).
+    static constexpr int kBlocksPerCu = 160 * 1024 / kLdsBytes;
+    // Waves per SIMD the register budget must allow: two co-resident 4-wave blocks need two, three need
+    // three (at most 168 VGPRs). Tiles that share a CU more ways stay far below their budget and keep the
+    // two-wave bound, which leaves the compiler's schedule for them as it is.
+    static constexpr int kWavesPerEu = kWaves <= 4 ? (kBlocksPerCu == 3 ? 3 : 2) : (kWaves + 3) / 4;
     static constexpr int kAInstr = kBM * kUnitsPerRow / kWave / kWaves;   // 1 KiB direct loads per wave
     static constexpr int kBInstr = U * kBN / kWave / kWaves;
     static_assert(U % 4 == 0, "a stage is a whole number of 64-deep MFMA groups");
@@ -687,33 +700,82 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
             a_lane[q][s2] = a_row_base * (S::kUnitsPerRow * 16) + (((8 * q + 2 * g + s2) ^ key) << 4);
     const int b_lane = g * S::kBN * 16 + b_col_base * 16;
 
-    auto compute = [&](const uint8_t* a_stage, const uint8_t* b_stage) {
-#pragma unroll
-        for (int q = 0; q < kGroups; ++q) {
+    // Two schedules of a stage's LDS reads. Reads first: the stage's reads all issue before its MFMAs (the
+    // scheduling barrier keeps the compiler from spreading them out), then one wait, the decode of every
+    // weight fragment, and the stage's MFMAs as one uninterrupted run. The waves of a SIMD belong to
+    // different blocks, so one wave's reads and decode overlap the others' MFMA runs: on a CU holding the
+    // tile's full complement of blocks that is 3-5% faster than the interleaved schedule (C3, C2), with
+    // fewer blocks per CU it is slower (a 128 x 256 block alone on its CU: ~18%; 128 x 128 tiles two per
+    // CU: 2-6%), hence the launcher's per-workgroup choice (reads_first_blocks). Interleaved: each k half's
+    // reads issue as its MFMAs need them. Reads first holds all of a stage's operands at once, up to
+    // 8 (RM + RN) more VGPRs: the bf16-activation variants of the larger wave tiles cannot spare them (they
+    // would spill), tiles sharing a CU four or more ways would lose a block per CU to them, and 8-wave
+    // blocks pair a SIMD's waves inside one block, in step.
+    constexpr bool kReadsFirst = kGroups == 1 && S::kWaves <= 4 && S::kBlocksPerCu >= 2 && S::kBlocksPerCu <= 3 &&
+                                 (!kABf16 || (RM <= 4 && RN <= 4));
+    auto compute = [&](auto reads_first, const uint8_t* a_stage, const uint8_t* b_stage) {
+        if constexpr (decltype(reads_first)::value) {
             u32x4 braw[RN];
+            u32x4 araw[2][RM];
 #pragma unroll
-            for (int j = 0; j < RN; ++j) {
-                braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + (4 * q * S::kBN + 16 * j) * 16);
-            }
+            for (int j = 0; j < RN; ++j) braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + 16 * j * 16);
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                half8 w[RN];
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-                for (int j = 0; j < RN; ++j) {
-                    half8 w0, w1;
-                    decode_chunk<kE5M2>(braw[j], w0, w1);
-                    w[j] = s2 == 0 ? w0 : w1;
-                }
+                for (int i = 0; i < RM; ++i)
+                    araw[s2][i] = *reinterpret_cast<const u32x4*>(a_stage + a_lane[0][s2] + i * 16 * S::kUnitsPerRow * 16);
+            __builtin_amdgcn_sched_barrier(0);
+            half8 w[2][RN];
+#pragma unroll
+            for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(braw[j], w[0][j], w[1][j]);
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                 for (int i = 0; i < RM; ++i) {
-                    const u32x4 raw = *reinterpret_cast<const u32x4*>(
-                        a_stage + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
-                    const half8 x = __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(raw) : raw);
+                    const half8 x =
+                        __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(araw[s2][i]) : araw[s2][i]);
 #pragma unroll
-                    for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
+                    for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[s2][j], x, acc[i][j]);
+                }
+        } else {
+#pragma unroll
+            for (int q = 0; q < kGroups; ++q) {
+                u32x4 braw[RN];
+#pragma unroll
+                for (int j = 0; j < RN; ++j) {
+                    braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + (4 * q * S::kBN + 16 * j) * 16);
+                }
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    half8 w[RN];
+#pragma unroll
+                    for (int j = 0; j < RN; ++j) {
+                        half8 w0, w1;
+                        decode_chunk<kE5M2>(braw[j], w0, w1);
+                        w[j] = s2 == 0 ? w0 : w1;
+                    }
+#pragma unroll
+                    for (int i = 0; i < RM; ++i) {
+                        const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                            a_stage + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
+                        const half8 x = __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(raw) : raw);
+#pragma unroll
+                        for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
+                    }
                 }
             }
         }
+    };
+    // Runs `loop` with the schedule this workgroup takes; one copy of the loop per schedule.
+    const bool reads_first = static_cast<int>(blockIdx.x) < p.reads_first_blocks;
+    auto with_schedule = [&](auto loop) {
+        if constexpr (kReadsFirst) {
+            if (reads_first) {
+                loop(Flag<true>{});
+                return;
+            }
+        }
+        loop(Flag<false>{});
     };
 
     if constexpr (kStageA) {
@@ -727,29 +789,32 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
             if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
         }
         commit_a(0);
-        for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
+        with_schedule([&](auto reads_first) {
+            for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
 #pragma unroll
-            for (int b = 0; b < S::kPeriod; ++b) {
-                const int t = t0 + b;
-                if (t < stages) {
-                    if constexpr (S::kLeadB == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-                    // This wave's LDS writes of A(t) are done; the barrier publishes every wave's and
-                    // retires all reads of the slots refilled next (they held stage t - 1).
-                    __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
-                    barrier_only();
-                    __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
-                    if (t + 1 < stages) load_a(t + 1);
-                    if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                    __builtin_amdgcn_s_setprio(0);
-                    compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
-                    // The widening and LDS writes of the next stage's activations run at raised priority
-                    // too: they gate this block's next barrier (measured +5% on a bf16 128 x 256 tile).
-                    __builtin_amdgcn_s_setprio(1);
-                    if (t + 1 < stages) commit_a((b + 1) % S::kSlotsA);
-                    __builtin_amdgcn_s_setprio(0);
+                for (int b = 0; b < S::kPeriod; ++b) {
+                    const int t = t0 + b;
+                    if (t < stages) {
+                        if constexpr (S::kLeadB == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                        // This wave's LDS writes of A(t) are done; the barrier publishes every wave's and
+                        // retires all reads of the slots refilled next (they held stage t - 1).
+                        __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
+                        barrier_only();
+                        __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
+                        if (t + 1 < stages) load_a(t + 1);
+                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                        __builtin_amdgcn_s_setprio(0);
+                        compute(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
+                        // The widening and LDS writes of the next stage's activations run at raised priority
+                        // too: they gate this block's next barrier (measured +5% on a bf16 128 x 256 tile).
+                        __builtin_amdgcn_s_setprio(1);
+                        if (t + 1 < stages) commit_a((b + 1) % S::kSlotsA);
+                        __builtin_amdgcn_s_setprio(0);
+                    }
                 }
             }
-        }
+        });
     } else {
         // Prologue: iterations -LB .. -1 of the issue pattern.
 #pragma unroll
@@ -759,26 +824,29 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
         }
 
         // One period of both rings per outer iteration, so every slot is a compile-time offset.
-        for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
+        with_schedule([&](auto reads_first) {
+            for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
 #pragma unroll
-            for (int b = 0; b < S::kPeriod; ++b) {
-                const int t = t0 + b;
-                if (t < stages) {
-                    // Stage t's loads are complete for this wave; the barrier then makes every wave's share
-                    // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
-                    wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
-                    barrier_only();
-                    // The refills go out at raised wave priority, so a wave that just passed its barrier
-                    // issues them ahead of the co-resident block's MFMAs (measured +1.6% on a 128 x 256 tile;
-                    // raising it for the MFMAs instead lost).
-                    __builtin_amdgcn_s_setprio(1);
-                    if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
-                    if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                    __builtin_amdgcn_s_setprio(0);
-                    compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
+                for (int b = 0; b < S::kPeriod; ++b) {
+                    const int t = t0 + b;
+                    if (t < stages) {
+                        // Stage t's loads are complete for this wave; the barrier then makes every wave's share
+                        // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
+                        wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
+                        barrier_only();
+                        // The refills go out at raised wave priority, so a wave that just passed its barrier
+                        // issues them ahead of the co-resident block's MFMAs (measured +1.6% on a 128 x 256
+                        // tile; raising it for the MFMAs instead lost).
+                        __builtin_amdgcn_s_setprio(1);
+                        if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
+                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                        __builtin_amdgcn_s_setprio(0);
+                        compute(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
+                    }
                 }
             }
-        }
+        });
     }
 
     if constexpr (kSplitK) {

@@ -19,7 +19,6 @@ constexpr bool kE5M2 = FEATHER_B_E5M2 != 0;
 constexpr bool kABf16 = FEATHER_A_BF16 != 0;
 constexpr bool kOutBf16 = FEATHER_OUT_BF16 != 0;
 constexpr int kCus = 256;                // MI355X compute units
-constexpr int kLdsPerCu = 160 * 1024;    // LDS bytes per CU
 
 template <int WM, int WN, int U, int RM, int RN, int PF>
 bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
@@ -32,6 +31,18 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         const int64_t blocks = tiles * p.splits;
         const dim3 grid(static_cast<uint32_t>(blocks));
+        // Workgroups that take the ring kernel's reads-first schedule: it pays where a CU holds the tile's
+        // full complement of blocks. Workgroups dispatch in id order, breadth-first over the CUs, so that is
+        // every workgroup of a full round of kCus * per_cu, and all of a last, partial round that still fills
+        // some CUs (those end last); a partial round that fills none (at most per_cu - 1 blocks on any CU)
+        // keeps the interleaved schedule.
+        const auto with_rounds = [&](int per_cu) {
+            Params q = p;
+            const int64_t slots = int64_t{kCus} * per_cu;
+            const int64_t full = blocks / slots * slots;
+            q.reads_first_blocks = static_cast<int32_t>(blocks - full > int64_t{kCus} * (per_cu - 1) ? blocks : full);
+            return q;
+        };
         if constexpr (S::kBM <= 64 && (!kABf16 || WN <= 2)) {
             // A 64-row tile takes the deep ring when every block of the launch is resident at once with it
             // (as many blocks per CU as its LDS allows): there the deeper lead hides the memory latency that
@@ -39,23 +50,25 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
             // With bf16 activations the deep ring widens per fragment (each of the WN column waves widens
             // the block's rows again), which pays only while M <= 64 and WN <= 2.
             using D = DmaShape<WM, WN, U, RM, RN, true>;
-            if ((!kABf16 || p.M <= 64) && blocks <= int64_t{kCus} * (kLdsPerCu / D::kLdsBytes)) {
+            if ((!kABf16 || p.M <= 64) && blocks <= int64_t{kCus} * D::kBlocksPerCu) {
+                const Params q = with_rounds(D::kBlocksPerCu);
                 if (p.splits > 1) {
                     hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, true>), grid,
-                                       dim3(S::kThreads), 0, stream, p);
+                                       dim3(S::kThreads), 0, stream, q);
                 } else {
                     hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, true>),
-                                       grid, dim3(S::kThreads), 0, stream, p);
+                                       grid, dim3(S::kThreads), 0, stream, q);
                 }
                 return true;
             }
         }
+        const Params q = with_rounds(S::kBlocksPerCu);
         if (p.splits > 1) {
             hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, false>), grid,
-                               dim3(S::kThreads), 0, stream, p);
+                               dim3(S::kThreads), 0, stream, q);
         } else {
             hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, false>), grid,
-                               dim3(S::kThreads), 0, stream, p);
+                               dim3(S::kThreads), 0, stream, q);
         }
     } else {
         using S = StreamShape<WM, WN, U, RM, RN>;

@@ -158,6 +158,34 @@ def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
     check_against_oracle(out, a, bp, s, bias, rows=None if m < 1000 else sample_rows(m, n_random=16))
 
 
+@pytest.mark.parametrize("tile,n_tiles", [
+    ((2, 2, 4, 4, 8, 1), 132),   # 4 x 132 = 528 workgroups: a full round of 512 reads first, the 16 after it
+                                 # (one per CU) interleaved, in one launch
+    ((2, 2, 4, 4, 8, 1), 100),   # 400: a partial round that pairs blocks on some CUs, all reads first
+    ((2, 2, 4, 4, 8, 1), 60),    # 240: at most one block per CU, all interleaved
+    ((2, 2, 4, 4, 4, 1), 194),   # 776: a full round of 768 (three per CU) reads first, 8 interleaved
+    ((2, 2, 4, 4, 4, 1), 150),   # 600: some CUs hold three, all reads first
+    ((2, 2, 4, 4, 4, 1), 100),   # 400: at most two per CU, all interleaved
+])
+@pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
+def test_ring_operand_schedules(fo, tile, n_tiles, a_dtype):
+    """The ring kernel's two operand-read schedules (reads first on CUs holding the tile's full complement
+    of blocks, interleaved elsewhere, chosen per workgroup by the launcher from the grid): grids of 512
+    rows whose workgroup counts put the launch on one, the other or both, against the oracle on a row of
+    every 16-row fragment (so every tile, tail rounds included)."""
+    m, K = 512, 384                       # 4 row tiles, 6 stages: one period of both rings
+    bn = 16 * tile[1] * tile[4]
+    n = bn * n_tiles
+    a = _tensor((m, K), a_dtype)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((K, n), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.5, device="cuda")
+    out_dtype = a_dtype
+    bias = _tensor((n,), out_dtype, seed=2)
+    out = fo.scaled_mm_hip(a, bp, s, bias, out_dtype, tile=tile)
+    rows = np.array(sorted({16 * f + (7 * f) % 16 for f in range(m // 16)} | {0, m - 1}), dtype=np.int64)
+    check_against_oracle(out, a, bp, s, bias, rows=rows)
+
+
 # One cell per regime of the fitted heuristic (skinny split-K with 16/32/64 columns and 4/8 slices, split
 # across workgroups for long K, the 32-row streaming tile, the 64-row ring tiles for 16 < M <= 64 with a
 # big weight, split or not, the 64 x 64 ring tile for mid-size grids, and the
