@@ -700,44 +700,58 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
             a_lane[q][s2] = a_row_base * (S::kUnitsPerRow * 16) + (((8 * q + 2 * g + s2) ^ key) << 4);
     const int b_lane = g * S::kBN * 16 + b_col_base * 16;
 
-    // Two schedules of a stage's LDS reads. Reads first: the stage's reads all issue before its MFMAs (the
-    // scheduling barrier keeps the compiler from spreading them out), then one wait, the decode of every
-    // weight fragment, and the stage's MFMAs as one uninterrupted run. The waves of a SIMD belong to
-    // different blocks, so one wave's reads and decode overlap the others' MFMA runs: on a CU holding the
-    // tile's full complement of blocks that is 3-5% faster than the interleaved schedule (C3, C2), with
-    // fewer blocks per CU it is slower (a 128 x 256 block alone on its CU: ~18%; 128 x 128 tiles two per
-    // CU: 2-6%), hence the launcher's per-workgroup choice (reads_first_blocks). Interleaved: each k half's
-    // reads issue as its MFMAs need them. Reads first holds all of a stage's operands at once, up to
-    // 8 (RM + RN) more VGPRs: the bf16-activation variants of the larger wave tiles cannot spare them (they
-    // would spill), tiles sharing a CU four or more ways would lose a block per CU to them, and 8-wave
-    // blocks pair a SIMD's waves inside one block, in step.
+    // Two schedules of a stage's LDS reads. Reads first: right after the stage's barrier the wave issues all
+    // of the stage's LDS reads (RN weight and 2 RM activation fragments; a scheduling barrier keeps the
+    // compiler from spreading them out), then the stage's refills, then waits once, decodes every weight
+    // fragment and issues the stage's MFMAs as one uninterrupted run. The waves of a SIMD belong to
+    // different blocks, so one wave's reads, refills and decode run under the others' MFMA runs: on a CU
+    // holding the tile's full complement of blocks that is 3-5% faster than the interleaved schedule (C3,
+    // and C2 with the refills after the reads), with fewer blocks per CU it is slower (a 128 x 256 block
+    // alone on its CU: ~18%; 128 x 128 tiles two per CU: 2-6%), hence the launcher's per-workgroup choice
+    // (reads_first_blocks). Interleaved: the refills go out first, then each k half's reads issue as its
+    // MFMAs need them. Reads first holds all of a stage's operands at once, up to 8 (RM + RN) more VGPRs:
+    // the bf16-activation variants of the larger wave tiles cannot spare them (they would spill), tiles
+    // sharing a CU four or more ways would lose a block per CU to them, and 8-wave blocks pair a SIMD's
+    // waves inside one block, in step.
     constexpr bool kReadsFirst = kGroups == 1 && S::kWaves <= 4 && S::kBlocksPerCu >= 2 && S::kBlocksPerCu <= 3 &&
                                  (!kABf16 || (RM <= 4 && RN <= 4));
-    auto compute = [&](auto reads_first, const uint8_t* a_stage, const uint8_t* b_stage) {
+    struct StageOperands {
+        u32x4 b[RN];
+        u32x4 a[2][RM];
+    };
+    auto read_stage = [&](const uint8_t* a_stage, const uint8_t* b_stage, StageOperands& op) {
+#pragma unroll
+        for (int j = 0; j < RN; ++j) op.b[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + 16 * j * 16);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+                op.a[s2][i] = *reinterpret_cast<const u32x4*>(a_stage + a_lane[0][s2] + i * 16 * S::kUnitsPerRow * 16);
+    };
+    auto multiply_stage = [&](const StageOperands& op) {
+        half8 w[2][RN];
+#pragma unroll
+        for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(op.b[j], w[0][j], w[1][j]);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < RM; ++i) {
+                const half8 x =
+                    __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(op.a[s2][i]) : op.a[s2][i]);
+#pragma unroll
+                for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[s2][j], x, acc[i][j]);
+            }
+    };
+    // One stage of the ring loop after its barrier: `refill` issues the stage's refills.
+    auto run_stage = [&](auto reads_first, const uint8_t* a_stage, const uint8_t* b_stage, auto refill) {
         if constexpr (decltype(reads_first)::value) {
-            u32x4 braw[RN];
-            u32x4 araw[2][RM];
-#pragma unroll
-            for (int j = 0; j < RN; ++j) braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + 16 * j * 16);
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-                for (int i = 0; i < RM; ++i)
-                    araw[s2][i] = *reinterpret_cast<const u32x4*>(a_stage + a_lane[0][s2] + i * 16 * S::kUnitsPerRow * 16);
+            StageOperands op;
+            read_stage(a_stage, b_stage, op);
+            refill();
             __builtin_amdgcn_sched_barrier(0);
-            half8 w[2][RN];
-#pragma unroll
-            for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(braw[j], w[0][j], w[1][j]);
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-                for (int i = 0; i < RM; ++i) {
-                    const half8 x =
-                        __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(araw[s2][i]) : araw[s2][i]);
-#pragma unroll
-                    for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[s2][j], x, acc[i][j]);
-                }
+            multiply_stage(op);
         } else {
+            refill();
 #pragma unroll
             for (int q = 0; q < kGroups; ++q) {
                 u32x4 braw[RN];
@@ -800,12 +814,13 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                         // retires all reads of the slots refilled next (they held stage t - 1).
                         __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
                         barrier_only();
-                        __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
-                        if (t + 1 < stages) load_a(t + 1);
-                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                        __builtin_amdgcn_s_setprio(0);
-                        compute(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
-                                lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
+                        run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                  lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
+                                      __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
+                                      if (t + 1 < stages) load_a(t + 1);
+                                      if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                                      __builtin_amdgcn_s_setprio(0);
+                                  });
                         // The widening and LDS writes of the next stage's activations run at raised priority
                         // too: they gate this block's next barrier (measured +5% on a bf16 128 x 256 tile).
                         __builtin_amdgcn_s_setprio(1);
@@ -834,15 +849,16 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                         // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
                         wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
                         barrier_only();
-                        // The refills go out at raised wave priority, so a wave that just passed its barrier
-                        // issues them ahead of the co-resident block's MFMAs (measured +1.6% on a 128 x 256
-                        // tile; raising it for the MFMAs instead lost).
-                        __builtin_amdgcn_s_setprio(1);
-                        if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
-                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                        __builtin_amdgcn_s_setprio(0);
-                        compute(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
-                                lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
+                        // The refills go out at raised wave priority, so a wave issues them ahead of the
+                        // co-resident blocks' MFMAs (measured +1.6% on a 128 x 256 tile; raising it for the
+                        // MFMAs instead lost).
+                        run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                  lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
+                                      __builtin_amdgcn_s_setprio(1);
+                                      if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
+                                      if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                                      __builtin_amdgcn_s_setprio(0);
+                                  });
                     }
                 }
             }
