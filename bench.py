@@ -41,8 +41,8 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile without a
 # measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
-    ("c3", (2, 2, 4, 4, 8, 1)): (190814 * 2.0 + 98304 * 1.0) * 1024,
-    ("c4", (8, 1, 4, 1, 4, 0)): (29220 * 2.0 + 448 * 1.0) * 1024,
+    ("c3", (2, 2, 4, 4, 8, 1)): (184487 * 2.0 + 98304 * 1.0) * 1024,
+    ("c4", (8, 1, 4, 1, 4, 0)): (29218 * 2.0 + 448 * 1.0) * 1024,
 }
 
 
