@@ -42,6 +42,7 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # measurement reports null.
 MEASURED_TRAFFIC_BYTES = {
     ("c3", (2, 2, 4, 4, 8, 1)): (184487 * 2.0 + 98304 * 1.0) * 1024,
+    ("c3", (1, 4, 4, 8, 4, 1)): (185289 * 2.0 + 98304 * 1.0) * 1024,
     ("c4", (8, 1, 4, 1, 4, 0)): (29218 * 2.0 + 448 * 1.0) * 1024,
 }
 

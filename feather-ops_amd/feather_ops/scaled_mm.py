@@ -26,6 +26,12 @@ from .tiles import gemm_block_sizes, ring_is_deep, split_workspace_bytes
 
 # Tiles the heuristic can return, each an entry of `SCALED_MM_TILES` (gfx950 meaning in tiles.py).
 _TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
+# The same block as 4 column waves of 128 x 64: each wave decodes half as many weight fragments per stage
+# (32 byte moves instead of 64) for 16 activation reads instead of 8; with fp16 activations and the
+# reads-first schedule it measured 1.2% faster in geometric mean over the 41 grid cells that pick 128 x 256
+# (C3 +1 to +3%, none slower than -0.5%); with bf16 activations (no reads-first schedule for its 128-row wave
+# tile) it measured even.
+_TILE_RING_128x256_W64 = (1, 4, 4, 8, 4, 1)
 _TILE_RING_256x256 = (4, 2, 4, 4, 8, 1)
 _TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
 _TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
@@ -162,7 +168,8 @@ def select_scaled_mm_config(
     extra cells where the grid had few:
     - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
-      tiles with their measured full-grid rates).
+      tiles with their measured full-grid rates); the 128 x 256 block as 4 column waves of 128 x 64 with
+      fp16 activations, as 2 x 2 waves of 64 x 128 with bf16 ones.
     - M > 64 with a smaller grid and K >= 4096, once the 16-row streaming tile would read 216 MiB of
       weight or more (N * K bytes once per 16 rows, over the fraction of CU slots its blocks fill in their
       last round): the 64 x 128 ring tile (deep ring) up to 256 of its tiles, split along K
@@ -197,7 +204,8 @@ def select_scaled_mm_config(
     a_bf16 = a_dtype == torch.bfloat16
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
-        return min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
+        tile = min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
+        return _TILE_RING_128x256_W64 if tile == _TILE_RING_128x256 and not a_bf16 else tile
     min_reread = _BF16_RING_MIN_REREAD if a_bf16 else _RING_MIN_REREAD
     ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
     if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:

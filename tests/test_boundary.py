@@ -259,7 +259,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto_bf16(1040, 1536, 6144) == ((1, 4, 4, 4, 2, 1), 3)  # 204 tiles x 3 = 612
     assert auto_bf16(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)
     assert auto(1040, 1536, 6144)[1] == 2                          # fp16: two per CU at most
-    assert auto(4096, 12288, 3072) == ((2, 2, 4, 4, 8, 1), 1)   # full grids never split
+    assert auto(4096, 12288, 3072) == ((1, 4, 4, 8, 4, 1), 1)   # full grids never split
     assert auto(16, 14336, 4096)[1] == 1
     # skinny M, long K, fewer than 192 16 x 64 streaming tiles: that tile, split for about 192 workgroups
     assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 4, 0), 3)      # 64 tiles
@@ -312,7 +312,8 @@ def test_heuristic_picks_on_representative_cells():
     """The fitted rule's regimes, one cell each (the picks the tile sweep measured best or within noise)."""
     from feather_ops.scaled_mm import select_scaled_mm_config as pick
 
-    assert pick(4096, 12288, 3072) == (2, 2, 4, 4, 8, 1)   # C3: 3 full waves of 128 x 256
+    assert pick(4096, 12288, 3072) == (1, 4, 4, 8, 4, 1)   # C3: 3 full waves of 128 x 256 (128 x 64 waves)
+    assert pick(4096, 12288, 3072, torch.bfloat16) == (2, 2, 4, 4, 8, 1)   # bf16: 64 x 128 waves
     assert pick(4096, 3072, 3072) == (2, 2, 4, 4, 4, 1)    # C2: one full wave of 128 x 128
     assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
     assert pick(4112, 1024, 5120) == (1, 4, 4, 4, 2, 1)    # one partial wave: 64 x 128 ring tiles

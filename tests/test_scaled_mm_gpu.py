@@ -163,6 +163,7 @@ def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
                                  # (one per CU) interleaved, in one launch
     ((2, 2, 4, 4, 8, 1), 100),   # 400: a partial round that pairs blocks on some CUs, all reads first
     ((2, 2, 4, 4, 8, 1), 60),    # 240: at most one block per CU, all interleaved
+    ((1, 4, 4, 8, 4, 1), 132),   # the same block as 128 x 64 waves (reads first with fp16 activations only)
     ((2, 2, 4, 4, 4, 1), 194),   # 776: a full round of 768 (three per CU) reads first, 8 interleaved
     ((2, 2, 4, 4, 4, 1), 150),   # 600: some CUs hold three, all reads first
     ((2, 2, 4, 4, 4, 1), 100),   # 400: at most two per CU, all interleaved
