@@ -43,11 +43,20 @@ _TILE_STREAM_16x64 = (8, 1, 4, 1, 4, 0)
 _CUS = 256
 
 # Ring tiles for large grids: (tile, blocks resident per CU, steady-state TFLOP/s on a full grid), measured
-# with the tile sweep (feather-ops_amd/benchmarks) on the large cells of its grid.
+# with the tile sweep (feather-ops_amd/benchmarks) on the large cells of its grid. With fp16 activations the
+# 128 x 256 block runs as 128 x 64 waves and outpaces the 128 x 128 tile by more: refitted on the 76 large-grid
+# cells of the sweep, any 128 x 128 rate from 920 to 980 gives 0.9975 of the best candidate in geometric mean
+# (1030: 0.9956); with bf16 activations the fit keeps 1030 (0.9945).
 _RING_MODEL = (
     (_TILE_RING_128x256, 2, 1100.0),
     (_TILE_RING_256x256, 1, 1040.0),
     (_TILE_RING_128x128, 3, 1030.0),
+    (_TILE_RING_64x128, 3, 600.0),
+)
+_RING_MODEL_FP16 = (
+    (_TILE_RING_128x256_W64, 2, 1100.0),
+    (_TILE_RING_256x256, 1, 1040.0),
+    (_TILE_RING_128x128, 3, 960.0),
     (_TILE_RING_64x128, 3, 600.0),
 )
 
@@ -204,8 +213,7 @@ def select_scaled_mm_config(
     a_bf16 = a_dtype == torch.bfloat16
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
-        tile = min(_RING_MODEL, key=lambda entry: _ring_time(M, N, *entry))[0]
-        return _TILE_RING_128x256_W64 if tile == _TILE_RING_128x256 and not a_bf16 else tile
+        return min(_RING_MODEL if a_bf16 else _RING_MODEL_FP16, key=lambda entry: _ring_time(M, N, *entry))[0]
     min_reread = _BF16_RING_MIN_REREAD if a_bf16 else _RING_MIN_REREAD
     ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
     if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
