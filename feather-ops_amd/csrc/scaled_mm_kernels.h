@@ -715,43 +715,163 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
     // waves inside one block, in step.
     constexpr bool kReadsFirst = kGroups == 1 && S::kWaves <= 4 && S::kBlocksPerCu >= 2 && S::kBlocksPerCu <= 3 &&
                                  (!kABf16 || (RM <= 4 && RN <= 4));
-    struct StageOperands {
-        u32x4 b[RN];
-        u32x4 a[2][RM];
-    };
-    auto read_stage = [&](const uint8_t* a_stage, const uint8_t* b_stage, StageOperands& op) {
+    if constexpr (kReadsFirst) {
+        struct StageOperands {
+            u32x4 b[RN];
+            u32x4 a[2][RM];
+        };
+        auto read_stage = [&](const uint8_t* a_stage, const uint8_t* b_stage, StageOperands& op) {
 #pragma unroll
-        for (int j = 0; j < RN; ++j) op.b[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + 16 * j * 16);
+            for (int j = 0; j < RN; ++j) op.b[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + 16 * j * 16);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int i = 0; i < RM; ++i)
-                op.a[s2][i] = *reinterpret_cast<const u32x4*>(a_stage + a_lane[0][s2] + i * 16 * S::kUnitsPerRow * 16);
-    };
-    auto multiply_stage = [&](const StageOperands& op) {
-        half8 w[2][RN];
+                for (int i = 0; i < RM; ++i)
+                    op.a[s2][i] =
+                        *reinterpret_cast<const u32x4*>(a_stage + a_lane[0][s2] + i * 16 * S::kUnitsPerRow * 16);
+        };
+        auto multiply_stage = [&](const StageOperands& op) {
+            half8 w[2][RN];
 #pragma unroll
-        for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(op.b[j], w[0][j], w[1][j]);
+            for (int j = 0; j < RN; ++j) decode_chunk<kE5M2>(op.b[j], w[0][j], w[1][j]);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+            for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-            for (int i = 0; i < RM; ++i) {
-                const half8 x =
-                    __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(op.a[s2][i]) : op.a[s2][i]);
+                for (int i = 0; i < RM; ++i) {
+                    const half8 x =
+                        __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(op.a[s2][i]) : op.a[s2][i]);
 #pragma unroll
-                for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[s2][j], x, acc[i][j]);
+                    for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[s2][j], x, acc[i][j]);
+                }
+        };
+        // One stage of the ring loop after its barrier: `refill` issues the stage's refills.
+        auto run_stage = [&](auto reads_first, const uint8_t* a_stage, const uint8_t* b_stage, auto refill) {
+            if constexpr (decltype(reads_first)::value) {
+                StageOperands op;
+                read_stage(a_stage, b_stage, op);
+                refill();
+                __builtin_amdgcn_sched_barrier(0);
+                multiply_stage(op);
+            } else {
+                refill();
+#pragma unroll
+                for (int q = 0; q < kGroups; ++q) {
+                    u32x4 braw[RN];
+#pragma unroll
+                    for (int j = 0; j < RN; ++j) {
+                        braw[j] = *reinterpret_cast<const u32x4*>(b_stage + b_lane + (4 * q * S::kBN + 16 * j) * 16);
+                    }
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; ++s2) {
+                        half8 w[RN];
+#pragma unroll
+                        for (int j = 0; j < RN; ++j) {
+                            half8 w0, w1;
+                            decode_chunk<kE5M2>(braw[j], w0, w1);
+                            w[j] = s2 == 0 ? w0 : w1;
+                        }
+#pragma unroll
+                        for (int i = 0; i < RM; ++i) {
+                            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                                a_stage + a_lane[q][s2] + i * 16 * S::kUnitsPerRow * 16);
+                            const half8 x =
+                                __builtin_bit_cast(half8, (kABf16 && !kStageA) ? bf16x8_to_f16x8(raw) : raw);
+#pragma unroll
+                            for (int j = 0; j < RN; ++j) acc[i][j] = mfma16(w[j], x, acc[i][j]);
+                        }
+                    }
+                }
             }
-    };
-    // One stage of the ring loop after its barrier: `refill` issues the stage's refills.
-    auto run_stage = [&](auto reads_first, const uint8_t* a_stage, const uint8_t* b_stage, auto refill) {
-        if constexpr (decltype(reads_first)::value) {
-            StageOperands op;
-            read_stage(a_stage, b_stage, op);
-            refill();
-            __builtin_amdgcn_sched_barrier(0);
-            multiply_stage(op);
+        };
+        // Runs `loop` with the schedule this workgroup takes; one copy of the loop per schedule.
+        const bool reads_first = static_cast<int>(blockIdx.x) < p.reads_first_blocks;
+        auto with_schedule = [&](auto loop) {
+            if constexpr (kReadsFirst) {
+                if (reads_first) {
+                    loop(Flag<true>{});
+                    return;
+                }
+            }
+            loop(Flag<false>{});
+        };
+
+        if constexpr (kStageA) {
+            // Iteration u loads A(u + 1) into registers and issues B(u + LB); the prologue runs the same pattern
+            // for u = -LB .. -1, then commits A(0). With LB >= 2 every B(t) is issued before A(t), so the wait for
+            // A(t)'s registers in commit_a (placed by the compiler; loads retire in issue order) also retires
+            // B(t); with LB == 1, B(t) follows A(t) and the iteration waits for it explicitly.
+#pragma unroll
+            for (int u = -S::kLeadB; u < 0; ++u) {
+                if (u == -1) load_a(0);
+                if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
+            }
+            commit_a(0);
+            with_schedule([&](auto reads_first) {
+                for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
+#pragma unroll
+                    for (int b = 0; b < S::kPeriod; ++b) {
+                        const int t = t0 + b;
+                        if (t < stages) {
+                            if constexpr (S::kLeadB == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                            // This wave's LDS writes of A(t) are done; the barrier publishes every wave's and
+                            // retires all reads of the slots refilled next (they held stage t - 1).
+                            __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
+                            barrier_only();
+                            run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                      lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
+                                          __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
+                                          if (t + 1 < stages) load_a(t + 1);
+                                          if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                                          __builtin_amdgcn_s_setprio(0);
+                                      });
+                            // The widening and LDS writes of the next stage's activations run at raised priority
+                            // too: they gate this block's next barrier (measured +5% on a bf16 128 x 256 tile).
+                            __builtin_amdgcn_s_setprio(1);
+                            if (t + 1 < stages) commit_a((b + 1) % S::kSlotsA);
+                            __builtin_amdgcn_s_setprio(0);
+                        }
+                    }
+                }
+            });
         } else {
-            refill();
+            // Prologue: iterations -LB .. -1 of the issue pattern.
+#pragma unroll
+            for (int u = -S::kLeadB; u < 0; ++u) {
+                if (u + S::kLeadA >= 0 && u + S::kLeadA < stages) issue_a(u + S::kLeadA);
+                if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
+            }
+
+            // One period of both rings per outer iteration, so every slot is a compile-time offset.
+            with_schedule([&](auto reads_first) {
+                for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
+#pragma unroll
+                    for (int b = 0; b < S::kPeriod; ++b) {
+                        const int t = t0 + b;
+                        if (t < stages) {
+                            // Stage t's loads are complete for this wave; the barrier then makes every wave's share
+                            // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
+                            wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
+                            barrier_only();
+                            // The refills go out at raised wave priority, so a wave issues them ahead of the
+                            // co-resident blocks' MFMAs (measured +1.6% on a 128 x 256 tile; raising it for the
+                            // MFMAs instead lost).
+                            run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
+                                      lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
+                                          __builtin_amdgcn_s_setprio(1);
+                                          if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
+                                          if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                                          __builtin_amdgcn_s_setprio(0);
+                                      });
+                        }
+                    }
+                }
+            });
+        }
+    } else {
+        // Tiles without the reads-first schedule keep this form of the loop (the same interleaved
+        // schedule as run_stage's): the compiler's code for it, and the measured speed of those tiles
+        // (bf16 activations on 128 x 256: 1-3%), depend on it.
+        auto compute = [&](const uint8_t* a_stage, const uint8_t* b_stage) {
 #pragma unroll
             for (int q = 0; q < kGroups; ++q) {
                 u32x4 braw[RN];
@@ -778,32 +898,19 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                     }
                 }
             }
-        }
-    };
-    // Runs `loop` with the schedule this workgroup takes; one copy of the loop per schedule.
-    const bool reads_first = static_cast<int>(blockIdx.x) < p.reads_first_blocks;
-    auto with_schedule = [&](auto loop) {
-        if constexpr (kReadsFirst) {
-            if (reads_first) {
-                loop(Flag<true>{});
-                return;
-            }
-        }
-        loop(Flag<false>{});
-    };
+        };
 
-    if constexpr (kStageA) {
-        // Iteration u loads A(u + 1) into registers and issues B(u + LB); the prologue runs the same pattern
-        // for u = -LB .. -1, then commits A(0). With LB >= 2 every B(t) is issued before A(t), so the wait for
-        // A(t)'s registers in commit_a (placed by the compiler; loads retire in issue order) also retires
-        // B(t); with LB == 1, B(t) follows A(t) and the iteration waits for it explicitly.
+        if constexpr (kStageA) {
+            // Iteration u loads A(u + 1) into registers and issues B(u + LB); the prologue runs the same pattern
+            // for u = -LB .. -1, then commits A(0). With LB >= 2 every B(t) is issued before A(t), so the wait for
+            // A(t)'s registers in commit_a (placed by the compiler; loads retire in issue order) also retires
+            // B(t); with LB == 1, B(t) follows A(t) and the iteration waits for it explicitly.
 #pragma unroll
-        for (int u = -S::kLeadB; u < 0; ++u) {
-            if (u == -1) load_a(0);
-            if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
-        }
-        commit_a(0);
-        with_schedule([&](auto reads_first) {
+            for (int u = -S::kLeadB; u < 0; ++u) {
+                if (u == -1) load_a(0);
+                if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
+            }
+            commit_a(0);
             for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
 #pragma unroll
                 for (int b = 0; b < S::kPeriod; ++b) {
@@ -814,13 +921,11 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                         // retires all reads of the slots refilled next (they held stage t - 1).
                         __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
                         barrier_only();
-                        run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
-                                  lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
-                                      __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
-                                      if (t + 1 < stages) load_a(t + 1);
-                                      if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                                      __builtin_amdgcn_s_setprio(0);
-                                  });
+                        __builtin_amdgcn_s_setprio(1);  // see the unstaged loop below
+                        if (t + 1 < stages) load_a(t + 1);
+                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                        __builtin_amdgcn_s_setprio(0);
+                        compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
                         // The widening and LDS writes of the next stage's activations run at raised priority
                         // too: they gate this block's next barrier (measured +5% on a bf16 128 x 256 tile).
                         __builtin_amdgcn_s_setprio(1);
@@ -829,17 +934,15 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                     }
                 }
             }
-        });
-    } else {
-        // Prologue: iterations -LB .. -1 of the issue pattern.
+        } else {
+            // Prologue: iterations -LB .. -1 of the issue pattern.
 #pragma unroll
-        for (int u = -S::kLeadB; u < 0; ++u) {
-            if (u + S::kLeadA >= 0 && u + S::kLeadA < stages) issue_a(u + S::kLeadA);
-            if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
-        }
+            for (int u = -S::kLeadB; u < 0; ++u) {
+                if (u + S::kLeadA >= 0 && u + S::kLeadA < stages) issue_a(u + S::kLeadA);
+                if (u + S::kLeadB < stages) issue_b(u + S::kLeadB);
+            }
 
-        // One period of both rings per outer iteration, so every slot is a compile-time offset.
-        with_schedule([&](auto reads_first) {
+            // One period of both rings per outer iteration, so every slot is a compile-time offset.
             for (int t0 = 0; t0 < stages; t0 += S::kPeriod) {
 #pragma unroll
                 for (int b = 0; b < S::kPeriod; ++b) {
@@ -849,20 +952,18 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
                         // visible and retires all reads of the slots the next issues reuse (they held stage t - 1).
                         wait_ring_stage<S::kLeadA, S::kLeadB, S::kAInstr, S::kBInstr>(stages - 1 - t);
                         barrier_only();
-                        // The refills go out at raised wave priority, so a wave issues them ahead of the
-                        // co-resident blocks' MFMAs (measured +1.6% on a 128 x 256 tile; raising it for the
-                        // MFMAs instead lost).
-                        run_stage(reads_first, lds + (b % S::kSlotsA) * S::kABytes,
-                                  lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes, [&] {
-                                      __builtin_amdgcn_s_setprio(1);
-                                      if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
-                                      if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
-                                      __builtin_amdgcn_s_setprio(0);
-                                  });
+                        // The refills go out at raised wave priority, so a wave that just passed its barrier
+                        // issues them ahead of the co-resident block's MFMAs (measured +1.6% on a 128 x 256 tile;
+                        // raising it for the MFMAs instead lost).
+                        __builtin_amdgcn_s_setprio(1);
+                        if (t + S::kLeadA < stages) issue_a(t + S::kLeadA);
+                        if (t + S::kLeadB < stages) issue_b(t + S::kLeadB);
+                        __builtin_amdgcn_s_setprio(0);
+                        compute(lds + (b % S::kSlotsA) * S::kABytes, lds + S::kBRing + (b % S::kSlotsB) * S::kBBytes);
                     }
                 }
             }
-        });
+        }
     }
 
     if constexpr (kSplitK) {
