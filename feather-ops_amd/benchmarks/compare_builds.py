@@ -57,6 +57,7 @@ def run_cell(libs: dict, m: int, n: int, k: int, args) -> dict:
     scale = torch.tensor(2.34, device="cuda", dtype=torch.float32)
     tile = tuple(args.tile) if args.tile else tuple(select_scaled_mm_config(m, n, k, a_dtype, fp8, a_dtype))
     splits = 1 if args.tile else select_scaled_mm_splits(m, n, k, tile, a_dtype)
+    tiles = {"new": tile, "old": tuple(args.old_tile) if args.old_tile else tile}
     stream = torch.cuda.current_stream().cuda_stream
     outs = {name: torch.empty((m, n), device="cuda", dtype=a_dtype) for name in libs}
     ws_bytes = split_workspace_bytes(m, n, k, tile, splits) if splits > 1 else 0
@@ -64,7 +65,7 @@ def run_cell(libs: dict, m: int, n: int, k: int, args) -> dict:
     bf16 = a_dtype == torch.bfloat16
 
     def provider(name):
-        lib, out, ws = libs[name], outs[name], workspaces[name]
+        lib, out, ws, tile = libs[name], outs[name], workspaces[name], tiles[name]
 
         def launch(_i):
             if splits > 1:
@@ -84,8 +85,8 @@ def run_cell(libs: dict, m: int, n: int, k: int, args) -> dict:
                   target_ms=args.target_ms)
     same = torch.equal(outs["new"].view(torch.int16), outs["old"].view(torch.int16))
     new_ms, old_ms = res["new"].median_ms, res["old"].median_ms
-    return {"M": m, "N": n, "K": k, "tile": list(tile), "splits": splits, "new_us": new_ms * 1e3,
-            "old_us": old_ms * 1e3, "new_over_old": new_ms / old_ms, "bit_identical": same}
+    return {"M": m, "N": n, "K": k, "tile": list(tile), "old_tile": list(tiles["old"]), "splits": splits,
+            "new_us": new_ms * 1e3, "old_us": old_ms * 1e3, "new_over_old": new_ms / old_ms, "bit_identical": same}
 
 
 def main() -> int:
@@ -96,6 +97,8 @@ def main() -> int:
     p.add_argument("--groups", default="baseline", help="comma-separated groups of cells.py, or 'all'")
     p.add_argument("--ring-only", action="store_true", help="only cells whose pick is an LDS ring tile")
     p.add_argument("--tile", type=lambda s: [int(x) for x in s.split(",")], help="pin one tile for every cell")
+    p.add_argument("--old-tile", type=lambda s: [int(x) for x in s.split(",")],
+                   help="the control build's tile, if not the same (with --tile; unsplit launches)")
     p.add_argument("--a-dtype", choices=sorted(_DT), default="fp16")
     p.add_argument("--fp8", choices=sorted(_FP8), default="e5m2")
     p.add_argument("--warmup", type=int, default=10)
@@ -105,6 +108,9 @@ def main() -> int:
     args = p.parse_args()
     if not torch.cuda.is_available():
         print("no GPU", file=sys.stderr)
+        return 1
+    if args.old_tile and not args.tile:
+        print("--old-tile needs --tile", file=sys.stderr)
         return 1
     if args.cells:
         todo = [tuple(int(x) for x in c.split(",")) for c in args.cells.split(";") if c.strip()]
@@ -124,8 +130,10 @@ def main() -> int:
                 continue
         r = run_cell(libs, m, n, k, args)
         rows.append(r)
-        print(f"{m}x{n}x{k} tile {tuple(r['tile'])} s{r['splits']}: new {r['new_us']:.2f} us  old {r['old_us']:.2f} us  "
-              f"new/old {r['new_over_old']:.3f}  {'bit-identical' if r['bit_identical'] else 'DIFFERENT'}", flush=True)
+        old_tile = "" if r["old_tile"] == r["tile"] else f" (old {tuple(r['old_tile'])})"
+        print(f"{m}x{n}x{k} tile {tuple(r['tile'])}{old_tile} s{r['splits']}: new {r['new_us']:.2f} us  "
+              f"old {r['old_us']:.2f} us  new/old {r['new_over_old']:.3f}  "
+              f"{'bit-identical' if r['bit_identical'] else 'DIFFERENT'}", flush=True)
     if rows:
         g = math.exp(sum(math.log(r["new_over_old"]) for r in rows) / len(rows))
         print(f"geomean new/old over {len(rows)} cells: {g:.4f} (min {min(r['new_over_old'] for r in rows):.3f}, "
