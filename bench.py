@@ -14,7 +14,9 @@ time per step.
 Also reported: the skinny HBM-bound cell C4 (A fp16 [16, 4096] x W e5m2 [14336, 4096]) as GB/s of
 algorithmic bytes, timed over a HIP graph of launches that rotate over 8 distinct weight copies (8 x
 58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2, the C3 shape
-with e4m3fn weights, two split-K cells with the unsplit tile beside each, and `cpu_baseline`: the
+with e4m3fn weights, the C3 shape with bf16 activations through the auto path (which widens them in a pass
+of their own there and runs the fp16-activation kernel; the in-place widening's time beside it), two
+split-K cells with the unsplit tile beside each, and `cpu_baseline`: the
 reference's CPU path (naive.py's semantics as torch CPU calls with fp32 accumulation) on C1, the
 CPU configuration, on the host's cores.
 
@@ -168,6 +170,36 @@ def time_square_cell(m: int, k: int, n: int, a_fmt: str, fp8: str, steps: int, w
 
     t = steady_rounds(launch_round, steps, rounds, warmup, min_warm_s=0.5)
     return {"tile": list(tile), **_cell_stats(t, 2.0 * m * n * k, algorithmic_bytes(m, k, n))}
+
+
+def time_bf16_auto_cell(m: int, k: int, n: int, steps: int, warmup: int, rounds: int):
+    """bf16 activations through the auto path (`scaled_mm_hip` without a tile: widened first, then the
+    fp16-activation kernel, where the heuristic says so) against the kernel widening them in place on the bf16
+    pick, back-to-back launches, steady state."""
+    import torch
+
+    import feather_ops
+    from feather_ops.scaled_mm import _auto_choice
+
+    a, bs, s = make_device_inputs(m, k, n, "bf16")
+    tile, splits, widen = _auto_choice(m, n, k, a.dtype)
+    in_tile = feather_ops.select_scaled_mm_config(m, n, k, a.dtype, bs[0].dtype, torch.bfloat16)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    op = torch.ops.feather_ops.scaled_mm.default
+
+    def auto_round():
+        for _ in range(steps):
+            feather_ops.scaled_mm_hip(a, bs[0], s, None, torch.bfloat16)
+
+    def in_place_round():
+        for _ in range(steps):
+            op(a, bs[0], s, None, out, *in_tile)
+
+    flops, nbytes = 2.0 * m * n * k, algorithmic_bytes(m, k, n)
+    auto = _cell_stats(steady_rounds(auto_round, steps, rounds, warmup, min_warm_s=0.5), flops, nbytes)
+    in_place = _cell_stats(steady_rounds(in_place_round, steps, rounds, warmup, min_warm_s=0.5), flops, nbytes)
+    return {"tile": list(tile), "splits": splits, "widened_first": widen, **auto,
+            "in_place_tile": list(in_tile), "in_place": in_place}
 
 
 def time_c4(rounds: int, copies: int = 8, replays: int = 10):
@@ -328,7 +360,7 @@ def main() -> int:
     parser.add_argument("--rounds", type=int, default=7, help="timed rounds of --steps launches (at least 5)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-secondary", action="store_true",
-                        help="skip the C4 (HBM), C2 (bf16), e4m3fn and split-K cells")
+                        help="skip the C4 (HBM), C2 (bf16), e4m3fn, bf16 auto-path and split-K cells")
     parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3"],
                         help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
@@ -354,6 +386,7 @@ def main() -> int:
     c4 = time_c4(rounds) if sec else None
     c2 = time_square_cell(4096, 3072, 3072, "bf16", "e5m2", 50, 10, rounds) if sec else None
     e4 = time_square_cell(4096, 3072, 12288, "fp16", "e4m3fn", 20, 10, rounds) if sec else None
+    bw = time_bf16_auto_cell(4096, 3072, 12288, 20, 10, rounds) if sec else None
     # 168 tiles of 128 x 128 for 256 CUs; the unsplit control is the best unsplit tile of the sweep
     sk = time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1), rounds) if sec else None
     # a decoder's down projection at batch 2: 64 tiles of 16 x 64, 67 MB of weight, 8 rotated copies; the
@@ -406,6 +439,10 @@ def main() -> int:
     if e4 is not None:
         line["e4m3_cell"] = {"workload": "C3 shape with e4m3fn weights: fp16 [4096,3072] x e4m3fn [12288,3072] -> fp16",
                              **e4, "frac_fp16_peak": round(e4["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
+    if bw is not None:
+        line["bf16_wide_cell"] = {"workload": "C3 shape with bf16 activations, auto path: bf16 [4096,3072] x e5m2 "
+                                              "[12288,3072] -> bf16 (widening pass included in the time)",
+                                  **bw, "frac_fp16_peak": round(bw["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
     if sk is not None:
         line["splitk_cell"] = {"workload": "underfilled grid: fp16 [512,5120] x e5m2 [5376,5120] -> fp16",
                                "tile": sk["tile"], "splits": sk["splits"], **sk["auto"],

@@ -18,7 +18,9 @@ Run from `feather-ops_amd/`:
     python -m benchmarks.benchmark_scaled_mm_hip --tiles --splits 2,3,4,6,8   # split-K candidates too
     python -m benchmarks.benchmark_scaled_mm_hip --groups text-16 --graph      # kernel time, no host gaps
 
-`auto` is the whole heuristic (tile and split count). With `--splits`, every listed tile (ring or
+`auto` is the whole heuristic (tile and split count, and for bf16 activations the widening pass where the
+auto path widens them first: then `auto` times that pass plus the fp16-activation pick, and `in_place` the bf16
+pick widening them inside the kernel, and the summary line gives auto's speedup over it). With `--splits`, every listed tile (ring or
 streaming) whose grid has fewer tiles than the GPU has compute units is also timed split `S` ways (named
 `(tile)/S`), for each `S` that keeps at most four workgroups per CU (`--split-any-grid`: whatever the
 grid, under that same cap). Every provider calls its op directly
@@ -40,6 +42,7 @@ sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
 from benchmarks.cells import GROUPS, cells  # noqa: E402
 from benchmarks.protocol import measure, paired_speedup  # noqa: E402
 from feather_ops.scaled_mm import (  # noqa: E402
+    _auto_choice,
     prepack_b_for_scaled_mm,
     select_scaled_mm_config,
     select_scaled_mm_splits,
@@ -99,6 +102,7 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
 
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, fp8, out_dtype))
     picked_splits = select_scaled_mm_splits(m, n, k, picked, a_dtype)
+    wide_tile, wide_splits, widen = _auto_choice(m, n, k, a_dtype)
     split_cases = [(tile, splits) for tile in tiles for splits in args.splits
                    if (_blocks(m, n, tile) < _CUS or args.split_any_grid) and _blocks(m, n, tile) * splits <= 4 * _CUS
                    and split_workspace_bytes(m, n, k, tile, splits) > 0]
@@ -121,16 +125,28 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     for tile, splits in split_cases:
         providers[f"{tile}/{splits}"] = launcher(tile, splits)
     auto_name = str(picked) if picked_splits == 1 else f"{picked}/{picked_splits}"
-    if auto_name not in providers:  # when the sweep includes the pick, `auto` is that measurement
+    if widen:
+        # bf16 activations the auto path widens first: `auto` is that pass plus the fp16-activation pick
+        # (unsplit), `in_place` the bf16 pick widening them inside the kernel
+        a16 = torch.empty((m, k), dtype=torch.float16, device="cuda")
+        widen_op = torch.ops.feather_ops.widen_bf16.default
+        providers["auto"] = lambda i: (widen_op(a, a16), op(a16, packs[i % copies], scale, bias, out, *wide_tile))
+        if auto_name not in providers:
+            providers["in_place"] = launcher(picked, picked_splits)
+    elif auto_name not in providers:  # when the sweep includes the pick, `auto` is that measurement
         providers["auto"] = launcher(picked, picked_splits)
     res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms, graph=args.graph)
     if "auto" not in res:
         res["auto"] = res[auto_name]
+    if widen and "in_place" not in res:
+        res["in_place"] = res[auto_name]
     tflops = {name: 2.0 * m * n * k / (r.median_ms * 1e-3) / 1e12 for name, r in res.items()}
     tile_names = [name for name in providers if name not in ("torch_mm", "auto")] or ["auto"]
     best = max(tile_names, key=lambda name: tflops[name])
     return {
         "M": m, "N": n, "K": k, "weight_copies": copies, "picked": list(picked), "picked_splits": picked_splits,
+        "widened_first": widen, "widened_tile": list(wide_tile) if widen else None,
+        "auto_vs_in_place": paired_speedup(res["auto"], res["in_place"]) if widen else None,
         "best": best,
         "tflops": tflops, "median_ms": {name: r.median_ms for name, r in res.items()},
         "spread": {name: (r.p80_ms - r.p20_ms) / r.median_ms for name, r in res.items()},
@@ -182,8 +198,9 @@ def main() -> int:
         t = r["tflops"]
         print(f"{group + ' ' + f'{m}x{n}x{k}':34s} {t['torch_mm']:9.1f} {t['auto']:9.1f} {t[r['best']]:9.1f}"
               f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])}"
-              f"{'/' + str(r['picked_splits']) if r['picked_splits'] > 1 else ''} -> {r['best']}",
-              flush=True)
+              f"{'/' + str(r['picked_splits']) if r['picked_splits'] > 1 else ''} -> {r['best']}"
+              + (f"  [widened first on {tuple(r['widened_tile'])}: x{r['auto_vs_in_place']:.3f} over in place]"
+                 if r["widened_first"] else ""), flush=True)
         if args.json_path:  # after every cell, so a run cut short keeps what it measured
             pathlib.Path(args.json_path).write_text(json.dumps({"args": vars(args), "results": results}, indent=1))
         torch.cuda.empty_cache()

@@ -181,8 +181,9 @@ void scaled_mm_splitk(const Tensor& a, const Tensor& b_prepacked, const std::opt
     check_launch(launched, "scaled_mm_splitk");
 }
 
-// feather_ops::bf16_to_fp16: out = bf16 -> fp16 (round toward zero) of x, both contiguous on one device.
-void bf16_to_fp16(const Tensor& x, Tensor& out) {
+// bf16 -> fp16 of x into out, both contiguous on one device: round toward zero (feather_ops::bf16_to_fp16,
+// the reference's bf16_to_fp16) or round to nearest even (feather_ops::widen_bf16, the activations' cast).
+void convert_bf16(const Tensor& x, Tensor& out, bool nearest, const char* name) {
     STD_TORCH_CHECK(x.is_cuda() && out.is_cuda(), "x and out must be CUDA tensors");
     STD_TORCH_CHECK(x.get_device_index() == out.get_device_index(), "x and out must be on one device");
     STD_TORCH_CHECK(x.scalar_type() == ST::BFloat16, "x must be bfloat16");
@@ -197,13 +198,19 @@ void bf16_to_fp16(const Tensor& x, Tensor& out) {
     torch::stable::accelerator::DeviceGuard guard(device_index);
     void* raw_stream = nullptr;
     TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &raw_stream));
-    const bool launched = feather_bf16_to_fp16(static_cast<const uint16_t*>(x.const_data_ptr()),
-                                               static_cast<uint16_t*>(out.mutable_data_ptr()), x.numel(),
-                                               static_cast<hipStream_t>(raw_stream));
-    STD_TORCH_CHECK(launched, "bf16_to_fp16: unsupported arguments");
+    const auto* in_bits = static_cast<const uint16_t*>(x.const_data_ptr());
+    auto* out_bits = static_cast<uint16_t*>(out.mutable_data_ptr());
+    const auto stream = static_cast<hipStream_t>(raw_stream);
+    const bool launched = nearest ? feather_widen_bf16(in_bits, out_bits, x.numel(), stream)
+                                  : feather_bf16_to_fp16(in_bits, out_bits, x.numel(), stream);
+    STD_TORCH_CHECK(launched, name, ": unsupported arguments");
     const hipError_t err = hipGetLastError();
-    STD_TORCH_CHECK(err == hipSuccess, "bf16_to_fp16 kernel launch failed: ", hipGetErrorString(err));
+    STD_TORCH_CHECK(err == hipSuccess, name, " kernel launch failed: ", hipGetErrorString(err));
 }
+
+void bf16_to_fp16(const Tensor& x, Tensor& out) { convert_bf16(x, out, false, "bf16_to_fp16"); }
+
+void widen_bf16(const Tensor& x, Tensor& out) { convert_bf16(x, out, true, "widen_bf16"); }
 
 // feather_ops::prepack_b: out[k // 16, n, k % 16] = b[k, n] for a [K, N] fp8 weight, K zero-padded to a
 // multiple of 128 (the reference's prepack_b_for_scaled_mm layout, feather_ops/scaled_mm.py:137-150).
@@ -247,6 +254,7 @@ STABLE_TORCH_LIBRARY(feather_ops, m) {
         "Tensor(b!) workspace, int splits, int block_warps_m, int block_warps_n, int unroll_k, int repeat_m, "
         "int repeat_n, bool prefetch=True) -> ()");
     m.def("bf16_to_fp16(Tensor x, Tensor(a!) out) -> ()");
+    m.def("widen_bf16(Tensor x, Tensor(a!) out) -> ()");
     m.def("prepack_b(Tensor b, Tensor(a!) out) -> ()");
 }
 
@@ -254,6 +262,7 @@ STABLE_TORCH_LIBRARY_IMPL(feather_ops, CUDA, m) {
     m.impl("scaled_mm", TORCH_BOX(&scaled_mm));
     m.impl("scaled_mm_splitk", TORCH_BOX(&scaled_mm_splitk));
     m.impl("bf16_to_fp16", TORCH_BOX(&bf16_to_fp16));
+    m.impl("widen_bf16", TORCH_BOX(&widen_bf16));
     m.impl("prepack_b", TORCH_BOX(&prepack_b));
 }
 

@@ -105,6 +105,21 @@ _STREAM_SPLIT_MAX_TILES = 171
 _STREAM_SPLIT_BLOCKS = 192
 _STREAM_SPLIT_MIN_RANGE = 2048
 
+# bf16 activations: the auto path widens them once up front (feather_ops::widen_bf16, the kernels' own
+# round-to-nearest-even conversion, so the result is the same bits) and runs the fp16-activation kernel when
+# that kernel's lead over widening in place repays the pass. Its lead, as a fraction of the fp16 kernel's
+# time, measured over the tile-sweep grid: 15-23% where the fp16 pick is the 128 x 256 block of 128 x 64 waves
+# (the bf16 form of that block runs 2 x 2 waves without the reads-first schedule: its register-staged
+# activations leave no room for it), 4-16% on the 128 x 128 and 64 x 128 tiles (taken here at the low end,
+# so no grid cell runs slower). The pass moves 4 bytes per activation element at ~6.2 TB/s and costs at
+# least ~4 us of launch; the fp16 kernel's time is modelled at 1.2 PFLOP/s; the lead has to exceed the pass
+# by a fifth. Split launches keep the in-place widening.
+_WIDEN_LEAD = {_TILE_RING_128x256_W64: 0.17, _TILE_RING_128x128: 0.08, _TILE_RING_64x128: 0.08}
+_WIDEN_FLOPS = 1.2e15
+_WIDEN_BYTES_PER_S = 6.2e12
+_WIDEN_MIN_S = 4e-6
+_WIDEN_MARGIN = 1.2
+
 
 def _blocks(M: int, N: int, tile: tuple[int, ...]) -> int:
     bm, bn, _ = gemm_block_sizes(tile)
@@ -321,12 +336,30 @@ def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1,
     return splits, busy(splits)
 
 
+def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> bool:
+    """Whether bf16 activations of this shape are widened once up front and run on `tile` (the fp16-activation
+    pick, unsplit) rather than widened inside the kernel; not in the reference, whose kernel always widens in
+    place. Measured over the tile-sweep grid's 95 cells with M >= 256: 0.935 of the in-place time in geometric
+    mean (0.926 for the better of the two per cell), none slower; C3's shape with bf16 activations 0.88."""
+    lead = _WIDEN_LEAD.get(tuple(tile), 0.0) if splits == 1 else 0.0
+    kernel_s = 2.0 * M * N * K / _WIDEN_FLOPS
+    widen_s = max(_WIDEN_MIN_S, 4.0 * M * K / _WIDEN_BYTES_PER_S)
+    return lead * kernel_s > _WIDEN_MARGIN * widen_s
+
+
 @functools.lru_cache(maxsize=4096)
-def _auto_choice(M: int, N: int, K: int, a_dtype: torch.dtype) -> tuple[tuple[int, int, int, int, int, int], int]:
-    """(tile, splits) the heuristic picks for a shape, memoized: a model runs the same few shapes again
-    and again, and the auto path then skips the model arithmetic (1-5 us of Python per call)."""
+def _auto_choice(M: int, N: int, K: int,
+                 a_dtype: torch.dtype) -> tuple[tuple[int, int, int, int, int, int], int, bool]:
+    """(tile, splits, widen first) the heuristic picks for a shape, memoized: a model runs the same few shapes
+    again and again, and the auto path then skips the model arithmetic (1-5 us of Python per call). With
+    `widen first` the tile and splits are the fp16-activation pick."""
+    if a_dtype == torch.bfloat16:
+        tile = select_scaled_mm_config(M, N, K, torch.float16)
+        splits = select_scaled_mm_splits(M, N, K, tile, torch.float16)
+        if widen_first(M, N, K, tile, splits):
+            return tile, splits, True
     tile = select_scaled_mm_config(M, N, K, a_dtype)
-    return tile, select_scaled_mm_splits(M, N, K, tile, a_dtype)
+    return tile, select_scaled_mm_splits(M, N, K, tile, a_dtype), False
 
 
 # Split-K workspaces, one per (device, stream): the counter area at their start must be zero before a
@@ -374,7 +407,14 @@ def _launch(
     out: torch.Tensor,
     tile: tuple[int, int, int, int, int, int],
     splits: int = 1,
+    widen: bool = False,
 ) -> None:
+    if widen and a.is_cuda and a.dim() == 2 and a.is_contiguous():
+        # an fp16 copy of the bf16 activations, rounded as the kernels round them; activations the op would
+        # refuse are passed on as they are, so that it reports them as it does without the widening
+        wide = torch.empty(a.shape, dtype=torch.float16, device=a.device)
+        torch.ops.feather_ops.widen_bf16.default(a, wide)
+        a = wide
     if splits == 1:
         torch.ops.feather_ops.scaled_mm.default(a, b_prepacked, scale, bias, out, *tile)
         return

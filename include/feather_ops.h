@@ -108,6 +108,17 @@ int64_t feather_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int bloc
 bool feather_bf16_to_fp16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
 
 /*
+ * out[i] = bf16 -> fp16 of in[i] with round-to-nearest-even (overflow to +-inf, inf/NaN pass through), n
+ * elements, enqueued on `stream`: the cast feather_ops/naive.py:21 applies to bf16 activations
+ * (`a.to(torch.float16)`), and the conversion launch_scaled_mm applies when a_bf16 is true, bit for bit, so
+ * launch_scaled_mm over the widened copy with a_bf16 = false returns what it returns over the original with
+ * a_bf16 = true. No counterpart in the reference, whose kernel always widens in place; here the heuristic's
+ * launches widen once up front for wide weights, where the fp16-activation kernel's speed repays the pass.
+ * in/out 16-byte aligned, n < 2^30; returns false (nothing enqueued) otherwise.
+ */
+bool feather_widen_bf16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t stream);
+
+/*
  * b_prepacked[k / 16][n][k % 16] = b[k][n] for a [K, N] row-major fp8 weight b (the GEMM's B = W^T),
  * with the K_pad - K rows past K (K_pad = ceil(K / 128) * 128) written as zeros: the layout
  * launch_scaled_mm reads, produced on the GPU and enqueued on `stream`. Restates the reference's Python

@@ -109,6 +109,9 @@ static int refuse(void) {
     expect(feather_bf16_to_fp16(a, c, -1, NULL), false, "bf16_to_fp16 with n < 0");
     expect(feather_bf16_to_fp16(PTR(const uint16_t*, 0x100002), c, 16, NULL), false, "bf16_to_fp16 misaligned");
     expect(feather_bf16_to_fp16(a, c, 0, NULL), true, "bf16_to_fp16 with n == 0 (nothing to do)");
+    expect(feather_widen_bf16(a, c, -1, NULL), false, "widen_bf16 with n < 0");
+    expect(feather_widen_bf16(a, PTR(uint16_t*, 0x500008), 16, NULL), false, "widen_bf16 output misaligned");
+    expect(feather_widen_bf16(a, c, 0, NULL), true, "widen_bf16 with n == 0 (nothing to do)");
     expect(feather_prepack_b(b, PTR(uint8_t*, 0x700000), 64, 12, NULL), false, "prepack with N % 8 != 0");
     expect(feather_prepack_b(b, PTR(uint8_t*, 0x700008), 64, 16, NULL), false, "prepack output misaligned");
     if (failures == 0) printf("refusals ok\n");

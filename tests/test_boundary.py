@@ -29,8 +29,9 @@ def lib():
     handle.launch_scaled_mm.restype = ctypes.c_bool
     handle.launch_scaled_mm.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + \
         [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_void_p]
-    handle.feather_bf16_to_fp16.restype = ctypes.c_bool
-    handle.feather_bf16_to_fp16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    for name in ("feather_bf16_to_fp16", "feather_widen_bf16"):
+        getattr(handle, name).restype = ctypes.c_bool
+        getattr(handle, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     handle.feather_prepack_b.restype = ctypes.c_bool
     handle.feather_prepack_b.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_void_p]
@@ -49,7 +50,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     names = _declared()
-    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_prepack_b",
+    assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_widen_bf16", "feather_prepack_b",
                           "feather_scaled_mm_splitk", "feather_splitk_workspace_bytes",
                           "feather_scaled_mm_splitk_noalloc"}
     for name in names:
@@ -156,11 +157,15 @@ def test_splitk_workspace_bytes_match_the_python_formula(lib):
     assert ws(512, 5376, 5120, 4, 1, 4, 1, 4, True, 2) == -1  # no such ring tile
 
 
-def test_convert_c_abi_refuses_bad_arguments(lib):
-    assert lib.feather_bf16_to_fp16(A, C, -1, None) is False
-    assert lib.feather_bf16_to_fp16(A + 2, C, 16, None) is False
-    assert lib.feather_bf16_to_fp16(None, C, 16, None) is False
-    assert lib.feather_bf16_to_fp16(A, C, 0, None) is True  # nothing to do, nothing enqueued
+@pytest.mark.parametrize("name", ["feather_bf16_to_fp16", "feather_widen_bf16"])
+def test_convert_c_abi_refuses_bad_arguments(lib, name):
+    convert = getattr(lib, name)
+    assert convert(A, C, -1, None) is False
+    assert convert(A + 2, C, 16, None) is False
+    assert convert(A, C + 8, 16, None) is False
+    assert convert(None, C, 16, None) is False
+    assert convert(A, C, 1 << 30, None) is False
+    assert convert(A, C, 0, None) is True  # nothing to do, nothing enqueued
 
 
 @pytest.mark.parametrize("args", [
@@ -296,6 +301,32 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
                 tile = pick(m, n, k)
                 s = splits(m, n, k, tile)
                 assert 1 <= s <= 8 and (s == 1 or -(-k // 64) // s >= 16)
+
+
+def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
+    """The auto path's widen-first rule (fitted on the tile sweep's grid, bf16 in place against widened + fp16
+    pick): wide weights on the 128 x 256 block (C3's shape 0.88 of the in-place time, 8192^3 0.94), not C2,
+    C5 or the split and streaming regimes; fp16 activations never."""
+    from feather_ops.scaled_mm import _auto_choice, widen_first
+
+    bf = torch.bfloat16
+    w64 = (1, 4, 4, 8, 4, 1)
+    assert _auto_choice(4096, 12288, 3072, bf) == (w64, 1, True)
+    assert _auto_choice(8192, 8192, 8192, bf) == (w64, 1, True)
+    assert _auto_choice(4112, 16384, 3072, bf) == (w64, 1, True)         # 0.896 measured
+    assert _auto_choice(4096, 4608, 12288, bf) == ((2, 2, 4, 4, 4, 1), 1, False)  # 128 x 128 at N = 4608: 0.92,
+    # below the rule's margin for that tile
+    assert _auto_choice(4096, 3072, 3072, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C2: 1.057 if widened
+    assert _auto_choice(4097, 5120, 2560, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C5's largest: 1.025
+    assert _auto_choice(6416, 1536, 6144, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # narrow weight: 1.158
+    assert _auto_choice(9232, 1024, 5120, bf)[2] is False
+    assert _auto_choice(512, 5120, 5120, bf) == ((2, 2, 4, 4, 4, 1), 3, False)    # split: in place
+    assert _auto_choice(16, 14336, 4096, bf)[2] is False
+    assert _auto_choice(4096, 12288, 3072, torch.float16) == (w64, 1, False)
+    # the rule itself: a lead of 17% of the modelled fp16 time against 1.2x the pass (>= 4 us)
+    assert widen_first(4096, 12288, 3072, w64, 1) and not widen_first(4096, 12288, 3072, w64, 2)
+    assert not widen_first(4096, 12288, 3072, (2, 2, 4, 2, 2, 1), 1)   # no measured lead for that tile
+    assert not widen_first(256, 4096, 1024, w64, 1)                      # under the pass's 4 us
 
 
 def test_heuristic_returns_instantiated_tiles():

@@ -213,7 +213,8 @@ HEURISTIC_CELLS = [
     (4112, 1024, 5120),  # 64 x 128 ring tile, one partial wave
     (512, 1024, 1024),   # 4-slice streaming tile
     (9216, 2048, 2048),  # 128 x 128 (one full wave of blocks)
-    (2320, 6144, 6144),  # 128 x 256
+    (2320, 6144, 6144),  # 128 x 256 (bf16 activations: widened first, then 128 x 64 waves)
+    (2048, 8192, 2048),  # 128 x 256 (bf16 activations: widened first, then 128 x 64 waves)
 ]
 
 
@@ -222,18 +223,36 @@ HEURISTIC_CELLS = [
 def test_heuristic_regimes(fo, m, n, k, a_dtype):
     """The picks depend on the activation dtype (bf16 ones take the small-grid ring tiles later), so each
     cell runs the auto path with both."""
-    from feather_ops.scaled_mm import select_scaled_mm_config, select_scaled_mm_splits
+    from feather_ops.scaled_mm import _auto_choice
 
     a = _tensor((m, k), a_dtype)
     bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
     scale = torch.tensor(0.75, device="cuda", dtype=torch.float32)
     bias = _tensor((n,), torch.bfloat16, seed=2)
     out = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16)
-    tile = select_scaled_mm_config(m, n, k, a_dtype, torch.float8_e5m2, torch.bfloat16)
-    splits = select_scaled_mm_splits(m, n, k, tile, a_dtype)
+    tile, splits, widen = _auto_choice(m, n, k, a_dtype)
     rows = None if m * n * k <= (1 << 28) else sample_rows(m, n_random=16)
     res = check_against_oracle(out, a, bp, scale, bias, rows=rows)
-    print(f"{m}x{n}x{k} tile {tile}/{splits}: max_abs={res['max_abs']:.4g} bound={res['bound']:.4g}")
+    print(f"{m}x{n}x{k} tile {tile}/{splits}{' widened first' if widen else ''}: max_abs={res['max_abs']:.4g} "
+          f"bound={res['bound']:.4g}")
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072)])
+def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
+    """Where the auto path widens bf16 activations first and runs the fp16-activation kernel, its output is the
+    bits of the in-place widening on the same tile (the C ABI's only bf16 form), bias and per-column scale
+    included."""
+    from feather_ops.scaled_mm import _auto_choice
+
+    tile, splits, widen = _auto_choice(m, n, k, torch.bfloat16)
+    assert widen and splits == 1
+    a = _tensor((m, k), torch.bfloat16)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
+    bias = _tensor((n,), torch.bfloat16, seed=2)
+    for scale in (torch.tensor(0.75, device="cuda"), torch.rand(n, device="cuda") + 0.5):
+        auto = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16)
+        in_place = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile)
+        assert torch.equal(auto.view(torch.int16), in_place.view(torch.int16))
 
 
 # ---- BASELINE configurations (north-star recipe) -----------------------------------------------------------
