@@ -272,7 +272,8 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
     device-to-device copy of a 512 MiB buffer, whose FETCH_SIZE / WRITE_SIZE calibrate the counters
     (1 x 512 MiB read and 1 x 512 MiB written per launch); torch_c3: torch's fp16 matmul (hipBLASLt) on
     the C3 shape with the weight already dequantized to fp16, the library control a counter comparison
-    is made against.
+    is made against; bf16_c3: the auto path on the C3 shape with bf16 activations (the widening pass, then
+    the fp16-activation kernel).
     """
     import torch
 
@@ -283,6 +284,12 @@ def run_only(which: str, steps: int, warmup: int, tile=None) -> None:
         w = torch.randn(12288, 3072, device="cuda", dtype=torch.float16)
         for _ in range(warmup + steps):
             torch.mm(a, w.t())
+        torch.cuda.synchronize()
+        return
+    if which == "bf16_c3":
+        a, bs, s = make_device_inputs(4096, 3072, 12288, "bf16")
+        for _ in range(warmup + steps):
+            feather_ops.scaled_mm_hip(a, bs[0], s, None, torch.bfloat16)
         torch.cuda.synchronize()
         return
     if which == "copy":
@@ -361,7 +368,7 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the C4 (HBM), C2 (bf16), e4m3fn, bf16 auto-path and split-K cells")
-    parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3"],
+    parser.add_argument("--only", choices=["c3", "c4", "copy", "torch_c3", "bf16_c3"],
                         help="launch one kernel only (for profilers)")
     parser.add_argument("--tile", help="with --only: pin the tile, e.g. 2,4,4,8,4,1")
     args = parser.parse_args()

@@ -18,9 +18,10 @@ Run from `feather-ops_amd/`:
     python -m benchmarks.benchmark_scaled_mm_hip --tiles --splits 2,3,4,6,8   # split-K candidates too
     python -m benchmarks.benchmark_scaled_mm_hip --groups text-16 --graph      # kernel time, no host gaps
 
-`auto` is the whole heuristic (tile and split count, and for bf16 activations the widening pass where the
-auto path widens them first: then `auto` times that pass plus the fp16-activation pick, and `in_place` the bf16
-pick widening them inside the kernel, and the summary line gives auto's speedup over it). With `--splits`, every listed tile (ring or
+`auto` is the whole heuristic (tile and split count, and for bf16 activations whether to widen them in a
+pass of their own first). Where it widens first (on every cell with `--widen-all`), `widened` times that pass
+plus the fp16-activation pick and `in_place` the bf16 pick widening them inside the kernel, and the summary
+line gives the first's speedup over the second. With `--splits`, every listed tile (ring or
 streaming) whose grid has fewer tiles than the GPU has compute units is also timed split `S` ways (named
 `(tile)/S`), for each `S` that keeps at most four workgroups per CU (`--split-any-grid`: whatever the
 grid, under that same cap). Every provider calls its op directly
@@ -103,6 +104,12 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     picked = tuple(select_scaled_mm_config(m, n, k, a_dtype, fp8, out_dtype))
     picked_splits = select_scaled_mm_splits(m, n, k, picked, a_dtype)
     wide_tile, wide_splits, widen = _auto_choice(m, n, k, a_dtype)
+    # bf16 activations: time the widening pass + fp16-activation pick against the in-place bf16 pick where the
+    # heuristic widens first, or on every cell with --widen-all (the data its rule is fitted on)
+    compare_widen = a_dtype == torch.bfloat16 and (widen or args.widen_all)
+    if compare_widen and not widen:
+        wide_tile = tuple(select_scaled_mm_config(m, n, k, torch.float16))
+        wide_splits = select_scaled_mm_splits(m, n, k, wide_tile, torch.float16)
     split_cases = [(tile, splits) for tile in tiles for splits in args.splits
                    if (_blocks(m, n, tile) < _CUS or args.split_any_grid) and _blocks(m, n, tile) * splits <= 4 * _CUS
                    and split_workspace_bytes(m, n, k, tile, splits) > 0]
@@ -110,7 +117,8 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
         split_cases.append((picked, picked_splits))
     # One zeroed workspace for every split launch of the cell (each leaves its counters at zero), passed
     # to the op directly, so that a launch allocates nothing and can be captured.
-    ws_bytes = max([split_workspace_bytes(m, n, k, tile, splits) for tile, splits in split_cases], default=0)
+    ws_cases = split_cases + ([(wide_tile, wide_splits)] if compare_widen and wide_splits > 1 else [])
+    ws_bytes = max([split_workspace_bytes(m, n, k, tile, splits) for tile, splits in ws_cases], default=0)
     ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
     split_op = torch.ops.feather_ops.scaled_mm_splitk.default
 
@@ -125,28 +133,37 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     for tile, splits in split_cases:
         providers[f"{tile}/{splits}"] = launcher(tile, splits)
     auto_name = str(picked) if picked_splits == 1 else f"{picked}/{picked_splits}"
-    if widen:
-        # bf16 activations the auto path widens first: `auto` is that pass plus the fp16-activation pick
-        # (unsplit), `in_place` the bf16 pick widening them inside the kernel
+    if compare_widen:
+        # `widened`: the widening pass plus the fp16-activation pick; `in_place`: the bf16 pick widening the
+        # activations inside the kernel; `auto` is whichever of the two the heuristic runs
         a16 = torch.empty((m, k), dtype=torch.float16, device="cuda")
         widen_op = torch.ops.feather_ops.widen_bf16.default
-        providers["auto"] = lambda i: (widen_op(a, a16), op(a16, packs[i % copies], scale, bias, out, *wide_tile))
+
+        def widened(i):
+            widen_op(a, a16)
+            if wide_splits == 1:
+                op(a16, packs[i % copies], scale, bias, out, *wide_tile)
+            else:
+                split_op(a16, packs[i % copies], scale, bias, out, ws, wide_splits, *wide_tile)
+
+        providers["widened"] = widened
         if auto_name not in providers:
             providers["in_place"] = launcher(picked, picked_splits)
     elif auto_name not in providers:  # when the sweep includes the pick, `auto` is that measurement
         providers["auto"] = launcher(picked, picked_splits)
     res = measure(providers, warmup=args.warmup, rounds=args.rounds, target_ms=args.target_ms, graph=args.graph)
-    if "auto" not in res:
-        res["auto"] = res[auto_name]
-    if widen and "in_place" not in res:
+    if compare_widen and "in_place" not in res:
         res["in_place"] = res[auto_name]
+    if "auto" not in res:
+        res["auto"] = res["widened"] if widen else res["in_place"] if compare_widen else res[auto_name]
     tflops = {name: 2.0 * m * n * k / (r.median_ms * 1e-3) / 1e12 for name, r in res.items()}
     tile_names = [name for name in providers if name not in ("torch_mm", "auto")] or ["auto"]
     best = max(tile_names, key=lambda name: tflops[name])
     return {
         "M": m, "N": n, "K": k, "weight_copies": copies, "picked": list(picked), "picked_splits": picked_splits,
-        "widened_first": widen, "widened_tile": list(wide_tile) if widen else None,
-        "auto_vs_in_place": paired_speedup(res["auto"], res["in_place"]) if widen else None,
+        "widened_first": widen, "widened_tile": list(wide_tile) if compare_widen else None,
+        "widened_splits": wide_splits if compare_widen else None,
+        "widened_vs_in_place": paired_speedup(res["widened"], res["in_place"]) if compare_widen else None,
         "best": best,
         "tflops": tflops, "median_ms": {name: r.median_ms for name, r in res.items()},
         "spread": {name: (r.p80_ms - r.p20_ms) / r.median_ms for name, r in res.items()},
@@ -172,6 +189,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--rounds", type=int, default=5)
     parser.add_argument("--target-ms", type=float, default=20.0)
+    parser.add_argument("--widen-all", action="store_true",
+                        help="bf16 activations: time the widening pass + fp16-activation pick on every cell")
     parser.add_argument("--graph", action="store_true",
                         help="time replays of captured batches (kernel time without host launch overhead)")
     parser.add_argument("--json", dest="json_path", default=None)
@@ -199,8 +218,9 @@ def main() -> int:
         print(f"{group + ' ' + f'{m}x{n}x{k}':34s} {t['torch_mm']:9.1f} {t['auto']:9.1f} {t[r['best']]:9.1f}"
               f"  {r['auto_vs_best']:9.3f}  {r['auto_vs_torch_mm']:10.3f}  {tuple(r['picked'])}"
               f"{'/' + str(r['picked_splits']) if r['picked_splits'] > 1 else ''} -> {r['best']}"
-              + (f"  [widened first on {tuple(r['widened_tile'])}: x{r['auto_vs_in_place']:.3f} over in place]"
-                 if r["widened_first"] else ""), flush=True)
+              + (f"  [{'widened first' if r['widened_first'] else 'widened (not picked)'} on "
+                 f"{tuple(r['widened_tile'])}{'/' + str(r['widened_splits']) if r['widened_splits'] > 1 else ''}: "
+                 f"x{r['widened_vs_in_place']:.3f} over in place]" if r["widened_tile"] else ""), flush=True)
         if args.json_path:  # after every cell, so a run cut short keeps what it measured
             pathlib.Path(args.json_path).write_text(json.dumps({"args": vars(args), "results": results}, indent=1))
         torch.cuda.empty_cache()

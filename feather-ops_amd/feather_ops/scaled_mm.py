@@ -110,10 +110,10 @@ _STREAM_SPLIT_MIN_RANGE = 2048
 # that kernel's lead over widening in place repays the pass. Its lead, as a fraction of the fp16 kernel's
 # time, measured over the tile-sweep grid: 15-23% where the fp16 pick is the 128 x 256 block of 128 x 64 waves
 # (the bf16 form of that block runs 2 x 2 waves without the reads-first schedule: its register-staged
-# activations leave no room for it), 4-16% on the 128 x 128 and 64 x 128 tiles (taken here at the low end,
-# so no grid cell runs slower). The pass moves 4 bytes per activation element at ~6.2 TB/s and costs at
-# least ~4 us of launch; the fp16 kernel's time is modelled at 1.2 PFLOP/s; the lead has to exceed the pass
-# by a fifth. Split launches keep the in-place widening.
+# activations leave no room for it), 4-16% on the 128 x 128 and 64 x 128 tiles, where it varies by more than
+# the pass costs (taken here at the low end, so no grid cell runs slower). The pass moves 4 bytes per
+# activation element at ~6.2 TB/s and costs at least ~4 us of launch; the fp16 kernel's time is modelled at
+# 1.2 PFLOP/s; the lead has to exceed the pass by a fifth. Split launches keep the in-place widening.
 _WIDEN_LEAD = {_TILE_RING_128x256_W64: 0.17, _TILE_RING_128x128: 0.08, _TILE_RING_64x128: 0.08}
 _WIDEN_FLOPS = 1.2e15
 _WIDEN_BYTES_PER_S = 6.2e12
@@ -339,8 +339,9 @@ def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1,
 def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> bool:
     """Whether bf16 activations of this shape are widened once up front and run on `tile` (the fp16-activation
     pick, unsplit) rather than widened inside the kernel; not in the reference, whose kernel always widens in
-    place. Measured over the tile-sweep grid's 95 cells with M >= 256: 0.935 of the in-place time in geometric
-    mean (0.926 for the better of the two per cell), none slower; C3's shape with bf16 activations 0.88."""
+    place. On the tile-sweep grid (`benchmark_scaled_mm_hip --a-dtype bf16 --widen-all`, 112 cells) it widens
+    44 cells first, each faster than in place (1.02-1.23x, 1.15x in geometric mean; C3's shape 1.10-1.14x):
+    1.056x over the whole grid against 1.068x for the better form per cell."""
     lead = _WIDEN_LEAD.get(tuple(tile), 0.0) if splits == 1 else 0.0
     kernel_s = 2.0 * M * N * K / _WIDEN_FLOPS
     widen_s = max(_WIDEN_MIN_S, 4.0 * M * K / _WIDEN_BYTES_PER_S)
