@@ -237,6 +237,37 @@ def test_heuristic_regimes(fo, m, n, k, a_dtype):
           f"bound={res['bound']:.4g}")
 
 
+def test_bf16_widened_first_replays_in_a_graph(fo):
+    """The widen-first auto path captured in a HIP graph (the fp16 copy comes from the graph's pool) replays the
+    eager result, re-reading the activations each replay: they change between replays, with eager work and
+    synchronizations in between."""
+    from feather_ops.scaled_mm import _auto_choice
+
+    m, n, k = 2048, 8192, 2048
+    assert _auto_choice(m, n, k, torch.bfloat16)[2]
+    a = _tensor((m, k), torch.bfloat16)
+    inputs = [_tensor((m, k), torch.bfloat16, seed=s) for s in (3, 4, 5)]
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.5, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fo.scaled_mm_hip(a, bp, s, None, torch.bfloat16)
+    for x in inputs + inputs[:1]:
+        a.copy_(x)
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fo.scaled_mm_hip(x, bp, s, None, torch.bfloat16)  # eager work in between
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072)])
 def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
     """Where the auto path widens bf16 activations first and runs the fp16-activation kernel, its output is the
