@@ -410,7 +410,7 @@ def _launch(
     splits: int = 1,
     widen: bool = False,
 ) -> None:
-    if widen and a.is_cuda and a.dim() == 2 and a.is_contiguous():
+    if widen and a.is_cuda and a.dim() == 2 and a.is_contiguous() and a.numel() < (1 << 30):
         # an fp16 copy of the bf16 activations, rounded as the kernels round them; activations the op would
         # refuse are passed on as they are, so that it reports them as it does without the widening
         wide = torch.empty(a.shape, dtype=torch.float16, device=a.device)
