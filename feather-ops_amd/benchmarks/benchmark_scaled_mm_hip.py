@@ -68,9 +68,10 @@ def parse_tiles(text: str) -> list[tuple[int, ...]]:
     for chunk in text.split(";"):
         tile = tuple(int(v) for v in chunk.split(","))
         if len(tile) != 6:
-            raise SystemExit(f"a tile is six ints (warps_m, warps_n, unroll_k, repeat_m, repeat_n, prefetch): {chunk!r}")
+            raise SystemExit(f"--tiles entry {chunk!r} should hold 6 comma-separated integers "
+                             "(block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch)")
         if tile not in SCALED_MM_TILES:
-            raise SystemExit(f"not instantiated: {tile}")
+            raise SystemExit(f"{tile} is not one of the compiled tiles (feather_ops.tiles.SCALED_MM_TILES)")
         tiles.append(tile)
     return tiles
 

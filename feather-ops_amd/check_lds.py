@@ -59,13 +59,16 @@ def compile_asm(combo: str) -> str:
     ]
     result = subprocess.run(command, capture_output=True, text=True, check=False)
     if result.returncode != 0:
-        raise SystemExit(f"hipcc failed:\n{result.stderr[-4000:]}")
+        raise SystemExit(f"compiling {combo} for gfx950 exited with {result.returncode}; end of its stderr:\n"
+                         f"{result.stderr[-4000:]}")
     return result.stdout
 
 
 def audit(asm: str) -> tuple[int, list[tuple]]:
     """(instantiations checked, [(kernel, ints, bools, allocated, expected)] that disagree)."""
-    pattern = re.compile(r"(ring_dma_kernel|stream_kernel)I((?:Li\d+E)+)((?:Lb[01]E)+)")
+    # A kernel's mangled name carries its template arguments as `L<type><value>E` tokens after `I`: `i` for
+    # the int tile parameters, `b` for the bool flags.
+    kernel_re = re.compile(r"(ring_dma_kernel|stream_kernel)I(.*)")
     name, checked, bad = None, 0, []
     for line in asm.splitlines():
         kd = re.match(r"\s*\.amdhsa_kernel\s+(\S+)", line)
@@ -74,12 +77,13 @@ def audit(asm: str) -> tuple[int, list[tuple]]:
             continue
         if name is None or ".amdhsa_group_segment_fixed_size" not in line:
             continue
-        match = pattern.search(name)
+        match = kernel_re.search(name)
         name = None
         if not match:
             continue
-        ints = [int(v) for v in re.findall(r"Li(\d+)E", match.group(2))]
-        bools = [int(v) for v in re.findall(r"Lb([01])E", match.group(3))]
+        tokens = re.findall(r"L([ib])(\d+)E", match.group(2))
+        ints = [int(v) for kind, v in tokens if kind == "i"]
+        bools = [int(v) for kind, v in tokens if kind == "b"]
         allocated = int(line.split()[-1])
         expected = expected_bytes(match.group(1), ints, bools)
         checked += 1
@@ -99,7 +103,7 @@ def main() -> int:
         print("no kernel metadata found")
         return 1
     if not bad:
-        print("every allocation matches")
+        print("each instantiation allocates exactly its tile's LDS")
         return 0
     print(f"{len(bad)} mismatches (kernel, ints, bools, allocated, expected):")
     for entry in bad:

@@ -1,4 +1,4 @@
-"""Mixed-precision matmul against a prepacked fp8 weight on gfx950: `Y = (X @ W^T) * scale + bias`.
+"""gfx950 scaled matmul of fp16/bf16 activations by a prepacked fp8 weight, `Y = (X @ W^T) * scale + bias`.
 
 Drop-in for the reference's `feather_ops/scaled_mm.py` (same names, arguments and op boundary):
 `X` is fp16 or bf16 `[M, K]`, `W` is fp8e5m2 or fp8e4m3fn stored as `[K_pad/16, N, 16]` (see
@@ -438,7 +438,8 @@ def _scaled_mm_auto(
     bias: torch.Tensor | None,
     out: torch.Tensor,
 ) -> None:
-    """The heuristic behind an opaque boundary: `torch.compile` does not specialize on its branches."""
+    """The auto-picked launch inside one custom op: a compiled graph holds a single node for it, whichever
+    tile, split count or widening the shape leads to."""
     _launch(a, b_prepacked, scale, bias, out, *_auto_choice(a.shape[0], b_prepacked.shape[1], a.shape[1], a.dtype))
 
 
@@ -451,11 +452,11 @@ def scaled_mm_hip(
     tile: tuple[int, int, int, int, int, int] | None = None,
     splits: int | None = None,
 ) -> torch.Tensor:
-    """`(a @ b^T) * scale + bias` against the prepacked fp8 weight `b_prepacked`.
+    """Returns `a @ W^T`, times `scale`, plus `bias`, in `out_dtype`, for the fp8 weight W held prepacked
+    in `b_prepacked`.
 
-    `tile` defaults to the heuristic. It exists so a benchmark or a test can pin it. `splits` (not in the
-    reference) pins the split-K count; by default the heuristic picks it when `tile` is None and a pinned
-    tile runs unsplit.
+    Without `tile` the heuristic chooses the launch; passing one (as the tile sweeps and tests do) runs
+    exactly that tile, unsplit unless `splits` (not in the reference) asks for a split-K count.
 
     The heuristic's launch goes through the opaque custom op `feather_ops::scaled_mm_auto` while
     `torch.compile` traces (as in the reference, `scaled_mm.py:104-134`), and straight to the launcher in
@@ -478,7 +479,8 @@ def scaled_mm_hip(
 
 
 def prepack_b_for_scaled_mm(b: torch.Tensor) -> torch.Tensor:
-    """`[K, N]` fp8 -> `[K_pad/16, N, 16]`, the layout the kernel indexes (reference `scaled_mm.py:137-150`).
+    """Rearranges a `[K, N]` fp8 weight into the `[K_pad/16, N, 16]` order the kernels read (reference
+    `scaled_mm.py:137-150`).
 
     `K` is zero-padded to a multiple of 128, so a ragged K never needs a staging branch; element
     `[k // 16, n, k % 16]` of the result is `b[k, n]`. A contiguous e5m2 / e4m3fn weight on the GPU with
@@ -517,5 +519,5 @@ def prepack_transpose(w: torch.Tensor) -> torch.Tensor:
 
 
 def tile_shape(tile: tuple[int, ...]) -> tuple[int, int, int]:
-    """`(block_m, block_n, chunk_k)` of a tile."""
+    """Rows, columns and K depth per stage of one workgroup of `tile`, as `(block_m, block_n, chunk_k)`."""
     return gemm_block_sizes(tile)
