@@ -1,10 +1,11 @@
-"""Relabelling an existing module class so that a kernel can take over its `forward`.
+"""Class swaps that route a loaded module's `forward` through the gfx950 kernels.
 
-Drop-in for the reference's `feather_ops/modules.py:21-47`. A consumer loads a model with its own
-machinery and then gives selected module instances a class that puts a mixin in front of the class they
-already have. Parameters, buffers, module names and `state_dict` keys are untouched (only `__class__`
-changes), so this can run after a checkpoint is loaded. Which classes may be relabelled and what the
-mixin's `forward` does is the consumer's policy, passed in as `accept` and `mixin`.
+Drop-in for the reference's `feather_ops/modules.py:21-47`. `relabelled_class(cls, mixin)` builds (once per
+pair) a subclass whose MRO is `mixin` then `cls`; `relabel_modules` assigns it as the `__class__` of the
+chosen instances of a model that is already built and loaded. Nothing else about an instance changes: its
+parameters, buffers, submodule names and `state_dict` keys stay as they were. The caller decides which
+instances qualify (`accept`) and what the mixin's `forward` does; `ScaledMMLinear` below is the mixin for
+`nn.Linear` on this path.
 """
 
 from collections.abc import Callable
