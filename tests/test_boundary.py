@@ -322,6 +322,11 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     assert _auto_choice(9232, 1024, 5120, bf)[2] is False
     assert _auto_choice(512, 5120, 5120, bf) == ((2, 2, 4, 4, 4, 1), 3, False)    # split: in place
     assert _auto_choice(16, 14336, 4096, bf)[2] is False
+    # M <= 64 on the 64 x 64 tile (the deep ring, which widens per fragment): big weights, split or not
+    assert _auto_choice(32, 25600, 5120, bf) == ((2, 2, 4, 2, 2, 1), 1, True)   # 1.19x measured
+    assert _auto_choice(32, 5120, 25600, bf) == ((2, 2, 4, 2, 2, 1), 6, True)   # 1.16-1.17x
+    assert _auto_choice(64, 16384, 4096, bf)[2] is False                         # 64 MB weight: 1.03x, kept
+    assert _auto_choice(32, 14336, 4096, bf)[2] is False                         # streaming tile: 0.89x
     assert _auto_choice(4096, 12288, 3072, torch.float16) == (w64, 1, False)
     # the rule itself: a lead of 17% of the modelled fp16 time against 1.2x the pass (>= 4 us)
     assert widen_first(4096, 12288, 3072, w64, 1) and not widen_first(4096, 12288, 3072, w64, 2)

@@ -268,21 +268,23 @@ def test_bf16_widened_first_replays_in_a_graph(fo):
         assert torch.equal(out.view(torch.int16), want.view(torch.int16))
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072)])
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072), (32, 25600, 5120),
+                                   (32, 5120, 25600)])
 def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
     """Where the auto path widens bf16 activations first and runs the fp16-activation kernel, its output is the
-    bits of the in-place widening on the same tile (the C ABI's only bf16 form), bias and per-column scale
-    included."""
+    bits of the in-place widening on the same tile and split count (the C ABI's only bf16 form), bias and
+    per-column scale included: the 128 x 256 block and, at 32 rows, the 64 x 64 deep ring unsplit and split
+    6 ways."""
     from feather_ops.scaled_mm import _auto_choice
 
     tile, splits, widen = _auto_choice(m, n, k, torch.bfloat16)
-    assert widen and splits == 1
+    assert widen
     a = _tensor((m, k), torch.bfloat16)
     bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
     bias = _tensor((n,), torch.bfloat16, seed=2)
     for scale in (torch.tensor(0.75, device="cuda"), torch.rand(n, device="cuda") + 0.5):
         auto = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16)
-        in_place = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile)
+        in_place = fo.scaled_mm_hip(a, bp, scale, bias, torch.bfloat16, tile=tile, splits=splits)
         assert torch.equal(auto.view(torch.int16), in_place.view(torch.int16))
 
 
