@@ -305,8 +305,9 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
 
 def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     """The auto path's widen-first rule (fitted on the tile sweep's grid, bf16 in place against widened + fp16
-    pick): wide weights on the 128 x 256 block (C3's shape 0.88 of the in-place time, 8192^3 0.94), not C2,
-    C5 or the split and streaming regimes; fp16 activations never."""
+    pick): wide weights on the 128 x 256 block (C3's shape 0.88 of the in-place time, 8192^3 0.94), long K on
+    the 128 x 128 tile, big weights on the 64 x 64 deep ring; not C2, C5 or the streaming regimes; fp16
+    activations never."""
     from feather_ops.scaled_mm import _auto_choice, widen_first
 
     bf = torch.bfloat16
@@ -314,8 +315,9 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     assert _auto_choice(4096, 12288, 3072, bf) == (w64, 1, True)
     assert _auto_choice(8192, 8192, 8192, bf) == (w64, 1, True)
     assert _auto_choice(4112, 16384, 3072, bf) == (w64, 1, True)         # 0.896 measured
-    assert _auto_choice(4096, 4608, 12288, bf) == ((2, 2, 4, 4, 4, 1), 1, False)  # 128 x 128 at N = 4608: 0.92,
-    # below the rule's margin for that tile
+    # 128 x 128: the lead grows with K (1.06-1.09x measured from K = 4608 on, 0.95-1.0x at K <= 3072)
+    assert _auto_choice(4096, 4608, 12288, bf) == ((2, 2, 4, 4, 4, 1), 1, True)    # 1.078-1.09x
+    assert _auto_choice(4608, 4096, 16384, bf) == ((2, 2, 4, 4, 4, 1), 1, True)    # 1.087-1.089x
     assert _auto_choice(4096, 3072, 3072, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C2: 1.057 if widened
     assert _auto_choice(4097, 5120, 2560, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C5's largest: 1.025
     assert _auto_choice(6416, 1536, 6144, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # narrow weight: 1.158
