@@ -111,16 +111,16 @@ _STREAM_SPLIT_MIN_RANGE = 2048
 # time, measured over the tile-sweep grid: 15-23% where the fp16 pick is the 128 x 256 block of 128 x 64 waves
 # (the bf16 form of that block runs 2 x 2 waves without the reads-first schedule: its register-staged
 # activations leave no room for it), 4-16% on the 128 x 128 and 64 x 128 tiles, where it varies by more than
-# the pass costs (taken at the low end, so no grid cell runs slower; on the 128 x 128 tile it grows with K:
-# 6-9% from K = 4608 on against 0-3% at K <= 2560 on two boxes, modelled as 0.14 (1 - 1024 / K)). The pass moves 4 bytes per
+# the pass costs (taken at the low end, so no grid cell runs slower; it grows with K: on 128 x 128 6-9% from
+# K = 4608 on against 0-3% at K <= 2560 on two boxes, modelled as 0.14 (1 - 1024 / K) for both tiles). The pass moves 4 bytes per
 # activation element at ~6.2 TB/s and costs at least ~4 us of launch; the fp16 kernel's time is modelled at
 # 1.2 PFLOP/s; the lead has to exceed the pass by a fifth. Split launches keep the in-place widening, except
 # on the 64 x 64 tile for M <= 64: that regime runs the deep ring, which widens bf16 per fragment after each
 # LDS read, and its lead is 17-22% (split or not) on weights of 100 MB and more (the pass costs its ~4 us
 # launch there), with the kernel's time set by the weight read (modelled at 4 TB/s).
-_WIDEN_LEAD = {_TILE_RING_128x256_W64: 0.17, _TILE_RING_64x128: 0.08}
-_WIDEN_LEAD_128x128 = 0.14
-_WIDEN_LEAD_128x128_K0 = 1024
+_WIDEN_LEAD_W64 = 0.17
+_WIDEN_LEAD_SMALL = 0.14   # the 128 x 128 and 64 x 128 tiles: times (1 - _WIDEN_LEAD_SMALL_K0 / K)
+_WIDEN_LEAD_SMALL_K0 = 1024
 _WIDEN_LEAD_DEEP_64x64 = 0.2
 _WIDEN_DEEP_MAX_M = 64
 _WIDEN_WEIGHT_BYTES_PER_S = 4e12
@@ -351,7 +351,8 @@ def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> b
     place. On the tile-sweep grid (`benchmark_scaled_mm_hip --a-dtype bf16 --widen-all`, 112 cells) it widens
     52 cells first, none slower than in place (1.01-1.23x, 1.14x in geometric mean; C3's shape 1.10-1.14x):
     1.063x over the whole grid against 1.068x for the better form per cell. That takes the 128 x 256 block
-    on wide weights, the 128 x 128 tile at long K (4096x4608x4608 1.08x, 4608x4096x16384 1.09x) and, with
+    on wide weights, the 128 x 128 and 64 x 128 tiles at long K (4096x4608x4608 1.08x, 4608x4096x16384 1.09x,
+    1072x5120x8192 1.11x) and, with
     M <= 64, the 64 x 64 tile on big weights (32x25600x5120 1.19x, 32x8192x28672 split 4 ways 1.22x)."""
     kernel_s = 2.0 * M * N * K / _WIDEN_FLOPS
     if M <= _WIDEN_DEEP_MAX_M and tuple(tile) == _TILE_RING_64x64:
@@ -359,10 +360,12 @@ def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> b
         kernel_s = max(kernel_s, N * K / _WIDEN_WEIGHT_BYTES_PER_S)
     elif splits > 1:
         lead = 0.0
-    elif tuple(tile) == _TILE_RING_128x128:
-        lead = max(0.0, _WIDEN_LEAD_128x128 * (1.0 - _WIDEN_LEAD_128x128_K0 / K))
+    elif tuple(tile) == _TILE_RING_128x256_W64:
+        lead = _WIDEN_LEAD_W64
+    elif tuple(tile) in (_TILE_RING_128x128, _TILE_RING_64x128):
+        lead = max(0.0, _WIDEN_LEAD_SMALL * (1.0 - _WIDEN_LEAD_SMALL_K0 / K))
     else:
-        lead = _WIDEN_LEAD.get(tuple(tile), 0.0)
+        lead = 0.0
     widen_s = max(_WIDEN_MIN_S, 4.0 * M * K / _WIDEN_BYTES_PER_S)
     return lead * kernel_s > _WIDEN_MARGIN * widen_s
 
