@@ -486,8 +486,9 @@ def test_op_rejects_bad_inputs(fo):
 
 
 # The reference's compile shapes (tests/test_scaled_mm_hip_compile.py:7), plus one the heuristic splits K on
-# (512 x 5376 x 5120: 128 x 128 tiles, 3 ways).
-@pytest.mark.parametrize("m,n,k", [(4112, 1152, 1152), (512, 1024, 5120), (512, 5376, 5120)])
+# (512 x 5376 x 5120: 128 x 128 tiles, 3 ways) and one whose bf16 activations the auto path widens first
+# (2048 x 8192 x 2048: the pass inside the custom op, then the 128 x 64-wave tile).
+@pytest.mark.parametrize("m,n,k", [(4112, 1152, 1152), (512, 1024, 5120), (512, 5376, 5120), (2048, 8192, 2048)])
 def test_compile_matches_eager(fo, m, n, k):
     """Reference tests/test_scaled_mm_hip_compile.py: one opaque node, eager == compiled."""
     for dynamic in (False, True):
