@@ -288,6 +288,41 @@ def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
         assert torch.equal(auto.view(torch.int16), in_place.view(torch.int16))
 
 
+def _random_cases(count: int = 16, seed: int = 11):
+    """Seeded shapes across the heuristic's regimes (M 1-9000, N and K multiples of 8 and 16 up to 14336), each
+    with its activation dtype, weight format, output dtype, bias and scale form."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(rng.choice([1, 7, 16, 40, 77, 300, 1000, 2048, 4097, 9000]))
+        n = int(rng.integers(1, 14336 // 8 + 1)) * 8
+        k = int(rng.integers(1, 14336 // 16 + 1)) * 16
+        if m * n * k > (1 << 37) or m * k > (1 << 25):
+            continue
+        cases.append((m, n, k, bool(rng.integers(2)), bool(rng.integers(2)), bool(rng.integers(2)),
+                      bool(rng.integers(2)), int(rng.integers(3))))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,a_bf16,e5m2,out_bf16,has_bias,scale_mode", _random_cases())
+def test_random_shapes_auto_path(fo, m, n, k, a_bf16, e5m2, out_bf16, has_bias, scale_mode):
+    """The whole auto path (tile, split count and, for bf16 activations, the widening pass) on seeded random
+    shapes and argument forms, against the oracle on sampled rows."""
+    from feather_ops.scaled_mm import _auto_choice
+
+    a_dtype = torch.bfloat16 if a_bf16 else torch.float16
+    out_dtype = torch.bfloat16 if out_bf16 else torch.float16
+    a = _tensor((m, k), a_dtype)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2 if e5m2 else torch.float8_e4m3fn, seed=1))
+    bias = _tensor((n,), out_dtype, seed=2) if has_bias else None
+    scale = [None, torch.tensor(0.75, device="cuda"), torch.rand(n, device="cuda") + 0.25][scale_mode]
+    out = fo.scaled_mm_hip(a, bp, scale, bias, out_dtype)
+    res = check_against_oracle(out, a, bp, scale, bias, rows=sample_rows(m, n_random=8))
+    tile, splits, widen = _auto_choice(m, n, k, a_dtype)
+    print(f"{m}x{n}x{k} {tile}/{splits}{' widened' if widen else ''}: max_abs={res['max_abs']:.4g} "
+          f"bound={res['bound']:.4g}")
+
+
 # ---- BASELINE configurations (north-star recipe) -----------------------------------------------------------
 
 CONFIGS = {
