@@ -11,7 +11,9 @@
  *       GPU: reads DIR/a.bin ([M, K] 16-bit bits), DIR/b.bin ([K, N] fp8 e5m2 codes, the unpacked weight),
  *       DIR/scale.bin (one fp32) and DIR/bias.bin ([N] output-dtype bits); prepacks the weight on the GPU
  *       (feather_prepack_b), runs launch_scaled_mm and feather_scaled_mm_splitk with SPLITS on a zeroed
- *       workspace, writes DIR/c.bin and DIR/c_split.bin, and prints the average time of 20 launches.
+ *       workspace, writes DIR/c.bin and DIR/c_split.bin, and prints the average time of 20 launches. With
+ *       A_BF16 it also widens the activations once (feather_widen_bf16) and runs launch_scaled_mm on the fp16
+ *       copy, writing DIR/c_widened.bin (the same bits as c.bin by the header's contract).
  */
 #include <hip/hip_runtime_api.h>
 
@@ -197,6 +199,24 @@ static int run(int argc, char** argv) {
     void* h_c = malloc(c_bytes);
     CHECK_HIP(hipMemcpy(h_c, d_c, c_bytes, hipMemcpyDeviceToHost));
     write_file(dir, "c.bin", h_c, c_bytes);
+
+    /* bf16 activations widened once up front, then the fp16-activation launch: the same output bits */
+    if (a_bf16) {
+        uint16_t* d_a16;
+        CHECK_HIP(hipMalloc((void**)&d_a16, a_bytes));
+        CHECK_HIP(hipMemset(d_c, 0, c_bytes));
+        if (!feather_widen_bf16(d_a, d_a16, M * K, stream) ||
+            !launch_scaled_mm(d_a16, d_p, d_s, d_bias, d_c, M, N, K, 1, 1, true, false, out_bf16, wm, wn, u, rm, rn,
+                              prefetch, stream)) {
+            fprintf(stderr, "feather_widen_bf16 or the launch after it refused the call\n");
+            return 1;
+        }
+        CHECK_HIP(hipGetLastError());
+        CHECK_HIP(hipStreamSynchronize(stream));
+        CHECK_HIP(hipMemcpy(h_c, d_c, c_bytes, hipMemcpyDeviceToHost));
+        write_file(dir, "c_widened.bin", h_c, c_bytes);
+        CHECK_HIP(hipFree(d_a16));
+    }
 
     /* the same product split along K, through a caller-owned workspace zeroed once */
     const int64_t ws_bytes = feather_splitk_workspace_bytes(M, N, K, wm, wn, u, rm, rn, prefetch, splits);

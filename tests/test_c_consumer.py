@@ -67,3 +67,6 @@ def test_consumer_runs_on_the_gpu(tmp_path, m, n, k, a_fmt, tile, splits):
         c_bits = np.fromfile(tmp_path / name, dtype=np.uint16).reshape(m, n)
         out = torch.from_numpy(c_bits.view(np.int16)).view(out_dt)
         check_against_oracle(out, a, bp, s, bias)
+    if a_fmt == oracle.BF16:  # widened once from C, then the fp16-activation launch: the in-place bits
+        assert np.array_equal(np.fromfile(tmp_path / "c_widened.bin", dtype=np.uint16),
+                              np.fromfile(tmp_path / "c.bin", dtype=np.uint16))
