@@ -336,6 +336,27 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     assert not widen_first(256, 4096, 1024, w64, 1)                      # under the pass's 4 us
 
 
+def test_widen_first_only_on_ring_tiles_with_a_measured_lead():
+    """Over seeded random shapes: the auto path widens bf16 activations first only onto the ring tiles whose lead
+    was measured (the 128 x 64-wave 128 x 256 block, 128 x 128 and 64 x 128 unsplit, and the 64 x 64 deep ring at
+    M <= 64, split or not), onto the fp16-activation pick, and never for fp16 activations."""
+    import numpy as np
+
+    from feather_ops.scaled_mm import _auto_choice
+
+    rng = np.random.default_rng(3)
+    ring_unsplit = {(1, 4, 4, 8, 4, 1), (2, 2, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1)}
+    for _ in range(400):
+        m = int(rng.integers(1, 20000))
+        n = int(rng.integers(1, 4000)) * 8
+        k = int(rng.integers(1, 1200)) * 16
+        assert _auto_choice(m, n, k, torch.float16)[2] is False
+        tile, splits, widen = _auto_choice(m, n, k, torch.bfloat16)
+        if widen:
+            assert (tile in ring_unsplit and splits == 1) or (tile == (2, 2, 4, 2, 2, 1) and m <= 64), (m, n, k, tile)
+            assert tile == _auto_choice(m, n, k, torch.float16)[0]
+
+
 def test_heuristic_returns_instantiated_tiles():
     from feather_ops.scaled_mm import select_scaled_mm_config
     from feather_ops.tiles import SCALED_MM_TILES
