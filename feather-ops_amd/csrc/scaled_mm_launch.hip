@@ -31,16 +31,20 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         const int64_t blocks = tiles * p.splits;
         const dim3 grid(static_cast<uint32_t>(blocks));
-        // Workgroups that take the ring kernel's reads-first schedule: it pays where a CU holds the tile's
-        // full complement of blocks. Workgroups dispatch in id order, breadth-first over the CUs, so that is
-        // every workgroup of a full round of kCus * per_cu, and all of a last, partial round that still fills
-        // some CUs (those end last); a partial round that fills none (at most per_cu - 1 blocks on any CU)
-        // keeps the interleaved schedule.
+        // Workgroups that take the ring kernel's reads-first schedule. Unsplit launches with fp16 activations
+        // take it everywhere: partial last rounds included, it measured 1-4% faster than the interleaved order
+        // there (same-box A/B, 128 x 256 and 128 x 128 tiles). With bf16 activations (register-staged) and in
+        // split launches it pays only where a CU holds the tile's full complement of blocks: workgroups
+        // dispatch in id order, breadth-first over the CUs, so that is every workgroup of a full round of
+        // kCus * per_cu, and all of a last, partial round that still fills some CUs (those end last); a
+        // partial round that fills none (at most per_cu - 1 blocks on any CU) keeps the interleaved schedule.
         const auto with_rounds = [&](int per_cu) {
             Params q = p;
             const int64_t slots = int64_t{kCus} * per_cu;
             const int64_t full = blocks / slots * slots;
-            q.reads_first_blocks = static_cast<int32_t>(blocks - full > int64_t{kCus} * (per_cu - 1) ? blocks : full);
+            const bool everywhere = !kABf16 && p.splits == 1;
+            q.reads_first_blocks = static_cast<int32_t>(
+                everywhere || blocks - full > int64_t{kCus} * (per_cu - 1) ? blocks : full);
             return q;
         };
         if constexpr (S::kBM <= 64 && (!kABf16 || WN <= 2)) {

@@ -158,18 +158,21 @@ def test_deep_and_shallow_ring_variants(fo, tile, m, n, splits, deep, a_dtype):
     check_against_oracle(out, a, bp, s, bias, rows=None if m < 1000 else sample_rows(m, n_random=16))
 
 
-@pytest.mark.parametrize("tile,n_tiles", [
-    ((2, 2, 4, 4, 8, 1), 132),   # 4 x 132 = 528 workgroups: a full round of 512 reads first, the 16 after it
-                                 # (one per CU) interleaved, in one launch
-    ((2, 2, 4, 4, 8, 1), 100),   # 400: a partial round that pairs blocks on some CUs, all reads first
-    ((2, 2, 4, 4, 8, 1), 60),    # 240: at most one block per CU, all interleaved
-    ((1, 4, 4, 8, 4, 1), 132),   # the same block as 128 x 64 waves (reads first with fp16 activations only)
-    ((2, 2, 4, 4, 4, 1), 194),   # 776: a full round of 768 (three per CU) reads first, 8 interleaved
-    ((2, 2, 4, 4, 4, 1), 150),   # 600: some CUs hold three, all reads first
-    ((2, 2, 4, 4, 4, 1), 100),   # 400: at most two per CU, all interleaved
+# Workgroup counts per launch, and the schedules they get with bf16 activations and in split launches
+# (unsplit launches with fp16 activations take reads first everywhere):
+@pytest.mark.parametrize("tile,n_tiles,splits", [
+    ((2, 2, 4, 4, 8, 1), 132, 1),   # 4 x 132 = 528 workgroups: a full round of 512 reads first, the 16 after it
+                                    # (one per CU) interleaved, in one launch
+    ((2, 2, 4, 4, 8, 1), 100, 1),   # 400: a partial round that pairs blocks on some CUs, all reads first
+    ((2, 2, 4, 4, 8, 1), 60, 1),    # 240: at most one block per CU, all interleaved
+    ((1, 4, 4, 8, 4, 1), 132, 1),   # the same block as 128 x 64 waves (reads first with fp16 activations only)
+    ((2, 2, 4, 4, 4, 1), 194, 1),   # 776: a full round of 768 (three per CU) reads first, 8 interleaved
+    ((2, 2, 4, 4, 4, 1), 150, 1),   # 600: some CUs hold three, all reads first
+    ((2, 2, 4, 4, 4, 1), 100, 1),   # 400: at most two per CU, all interleaved
+    ((2, 2, 4, 4, 4, 1), 97, 2),    # 776 split workgroups: 768 reads first, 8 interleaved, fp16 included
 ])
 @pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
-def test_ring_operand_schedules(fo, tile, n_tiles, a_dtype):
+def test_ring_operand_schedules(fo, tile, n_tiles, splits, a_dtype):
     """The ring kernel's two operand-read schedules (reads first on CUs holding the tile's full complement
     of blocks, interleaved elsewhere, chosen per workgroup by the launcher from the grid): grids of 512
     rows whose workgroup counts put the launch on one, the other or both, against the oracle on a row of
@@ -182,7 +185,7 @@ def test_ring_operand_schedules(fo, tile, n_tiles, a_dtype):
     s = torch.tensor(0.5, device="cuda")
     out_dtype = a_dtype
     bias = _tensor((n,), out_dtype, seed=2)
-    out = fo.scaled_mm_hip(a, bp, s, bias, out_dtype, tile=tile)
+    out = fo.scaled_mm_hip(a, bp, s, bias, out_dtype, tile=tile, splits=splits)
     rows = np.array(sorted({16 * f + (7 * f) % 16 for f in range(m // 16)} | {0, m - 1}), dtype=np.int64)
     check_against_oracle(out, a, bp, s, bias, rows=rows)
 
