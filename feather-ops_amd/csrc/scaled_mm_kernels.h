@@ -706,9 +706,11 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
     // fragment and issues the stage's MFMAs as one uninterrupted run. The waves of a SIMD belong to
     // different blocks, so one wave's reads, refills and decode run under the others' MFMA runs: on a CU
     // holding the tile's full complement of blocks that is 3-5% faster than the interleaved schedule (C3,
-    // and C2 with the refills after the reads), with fewer blocks per CU it is slower (a 128 x 256 block
-    // alone on its CU: ~18%; 128 x 128 tiles two per CU: 2-6%), hence the launcher's per-workgroup choice
-    // (reads_first_blocks). Interleaved: the refills go out first, then each k half's reads issue as its
+    // and C2 with the refills after the reads). Where CUs hold fewer blocks it measured slower when first
+    // built (a 128 x 256 block alone on its CU: ~18%; 128 x 128 tiles two per CU: 2-6%) and still is with
+    // bf16 activations and in split launches, hence the launcher's per-workgroup choice (reads_first_blocks);
+    // unsplit fp16 launches of the current kernel gain 1-4% from it there too and take it everywhere.
+    // Interleaved: the refills go out first, then each k half's reads issue as its
     // MFMAs need them. Reads first holds all of a stage's operands at once, up to 8 (RM + RN) more VGPRs:
     // the bf16-activation variants of the larger wave tiles cannot spare them (they would spill), tiles
     // sharing a CU four or more ways would lose a block per CU to them, and 8-wave blocks pair a SIMD's
