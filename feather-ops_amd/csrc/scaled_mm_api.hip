@@ -82,11 +82,13 @@ SplitLayout split_layout(int64_t M, int64_t N, int64_t K, int wm, int wn, int u,
 
 // Device memory of feather_scaled_mm_splitk_noalloc, in place of a caller's workspace: the same layout (the
 // 64 KiB counter area, then the partial sums), sized for split launches with up to 64 MiB of fp32 partials
-// (1024 workgroups of a 128 x 128 ring tile), the most the split heuristic launches. Every GPU the library
-// runs on holds its own copy until the process ends. Host code never passes `scratch` itself to a
+// (1024 workgroups of a 128 x 128 ring tile), the most the split heuristic launches. The array is part of the
+// code object, so every GPU the library is loaded onto reserves its own copy until the process ends, whether
+// or not the entry point is ever called. Host code never passes `scratch` itself to a
 // kernel (in host code the name is a stand-in, not a device address); it uses the address
 // hipGetSymbolAddress returns for the current device.
 constexpr int64_t kScratchBytes = kSplitCtrBytes + (int64_t{64} << 20);
+static_assert(kScratchBytes == FEATHER_NOALLOC_SCRATCH_BYTES, "the size the public header promises");
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;

@@ -75,17 +75,24 @@ bool feather_scaled_mm_splitk(const uint16_t* a, const uint8_t* b_prepacked, con
 /*
  * feather_scaled_mm_splitk without a workspace argument and without any allocation: the partial sums and
  * arrival counters live in a static device array of the library (64 KiB of counters + 64 MiB of partials on
- * each GPU it runs on, held until the process ends), so callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) can still split K. It calls
- * no hipMalloc, hipFree or allocating library routine; its first call on a device looks the array up
- * (hipGetSymbolAddress) and enqueues a small kernel on `stream` that zeroes the counters.
+ * each GPU it runs on), so callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc) can still split K. The array is part of the library's
+ * code object: loading the library onto a GPU reserves it there until the process ends, whether or not
+ * this function is ever called. It calls no hipMalloc, hipFree or allocating library routine; its first
+ * call on a device looks the array up (hipGetSymbolAddress) and enqueues a small kernel on `stream` that
+ * zeroes the counters. Make that first call on a device outside graph capture: later calls under capture
+ * record only the split launch, and each replay finds the counters zero, as every completed launch leaves
+ * them. (A first call made under capture records the clearing kernel into the graph ahead of the launch,
+ * and so does every captured call until one has run outside capture; it returns false if the runtime
+ * refuses the symbol lookup during capture.)
  *
  * No counterpart in the reference. Same arguments, contract and results as feather_scaled_mm_splitk,
  * minus the workspace. Returns false (nothing enqueued) where that function would, and also when the
  * launch needs more than the static array holds, i.e. when feather_splitk_workspace_bytes(...) exceeds
- * 65536 + 33554432 bytes. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * FEATHER_NOALLOC_SCRATCH_BYTES. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams or threads without ordering) race and must not be made.
  */
+#define FEATHER_NOALLOC_SCRATCH_BYTES (65536 + 67108864) /* 64 KiB of counters + 64 MiB of partial sums */
 bool feather_scaled_mm_splitk_noalloc(const uint16_t* a, const uint8_t* b_prepacked, const float* scale,
                                       const uint16_t* bias, uint16_t* c, int64_t M, int64_t N, int64_t K,
                                       int has_scale, int has_bias, bool use_fp8_e5m2, bool a_bf16, bool output_bf16,

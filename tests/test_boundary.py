@@ -112,10 +112,37 @@ def test_splitk_c_abi_refuses_out_of_contract_calls(lib, kwargs):
     assert _split(lib, **kwargs) is False
 
 
+def _header_scratch_bytes() -> int:
+    """FEATHER_NOALLOC_SCRATCH_BYTES as the public header defines it (a sum of decimal literals)."""
+    m = re.search(r"#define\s+FEATHER_NOALLOC_SCRATCH_BYTES\s+\(([\d\s+]+)\)", HEADER.read_text())
+    assert m, "include/feather_ops.h must define FEATHER_NOALLOC_SCRATCH_BYTES"
+    return sum(int(term) for term in m.group(1).split("+"))
+
+
+def test_header_scratch_size_is_the_librarys_refusal_threshold(lib):
+    """The static array size the header promises C callers is exactly where the library starts refusing: a
+    split launch needing FEATHER_NOALLOC_SCRATCH_BYTES of workspace is accepted, one needing more is not
+    (both refused or accepted on the host, before any GPU call). The accepted launch is not made here; its
+    size is only checked to sit at the threshold."""
+    scratch = _header_scratch_bytes()
+    assert scratch == 65536 + (64 << 20)
+    tile = (2, 2, 4, 4, 4, True)   # 128 x 128 ring tile: 64 KiB of fp32 partials per tile and split
+    # 1024 tiles x 1 x 64 KiB = exactly the partial area; the counters take the first 64 KiB
+    assert lib.feather_splitk_workspace_bytes(2048, 4096, 2560, *tile, 2) == scratch
+    # 8 more columns make 1056 tiles: past the array, refused before anything is enqueued
+    assert lib.feather_splitk_workspace_bytes(2048, 4104, 2560, *tile, 2) > scratch
+    assert lib.feather_scaled_mm_splitk_noalloc(A, B, S, BIAS, C, 2048, 4104, 2560, 1, 1, True, False, False,
+                                                *tile, 2, None) is False
+    # the Python heuristic keeps every split launch within the same array
+    from feather_ops.scaled_mm import _SPLIT_MAX_PARTIAL_BYTES
+
+    assert 65536 + _SPLIT_MAX_PARTIAL_BYTES == scratch
+
+
 def test_noalloc_splitk_refuses_past_its_static_array_and_out_of_contract(lib):
     """feather_scaled_mm_splitk_noalloc refuses, before any GPU call, a launch whose workspace would exceed
     its static array (64 KiB + 64 MiB), and everything feather_scaled_mm_splitk refuses."""
-    scratch = 65536 + (64 << 20)
+    scratch = _header_scratch_bytes()
     tile = (2, 2, 4, 4, 4, True)
 
     def call(m, n, k, splits, c=C):

@@ -367,13 +367,14 @@ def test_baseline_config(fo, name):
     s = torch.tensor(scale, dtype=torch.float32, device="cuda")
     out_dtype = torch.bfloat16 if a_fmt == oracle.BF16 else torch.float16
     out = fo.scaled_mm_hip(a, bp, s, None, out_dtype)
-    from feather_ops.scaled_mm import select_scaled_mm_config, select_scaled_mm_splits
+    from feather_ops.scaled_mm import _auto_choice
 
-    tile = select_scaled_mm_config(m, n, k, a.dtype, bp.dtype, out_dtype)
+    # the launch the auto path made: with widen first, the tile is the fp16-activation pick it ran
+    tile, splits, widen = _auto_choice(m, n, k, a.dtype)
     res = check_against_oracle(out, a, bp, s, None, rows=None)
     _log_parity({"config": name, "M": m, "K": k, "N": n, "a": a_fmt, "out": str(out_dtype).split(".")[-1],
-                 "outliers": outliers, "tile": list(tile),
-                 "splits": select_scaled_mm_splits(m, n, k, tile, a.dtype), "rows_checked": m,
+                 "outliers": outliers, "tile": list(tile), "splits": splits, "widened_first": widen,
+                 "rows_checked": m,
                  "max_abs": res["max_abs"], "rms": res["rms"], "bound": res["bound"], "strict_ok": res["strict_ok"],
                  "n_over": res["n_over"], "n_over_one_ulp": res["n_over_one_ulp"],
                  "n_band_flips": res.get("n_band_flips", 0), "n": res["n"]})

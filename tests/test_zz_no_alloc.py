@@ -98,3 +98,38 @@ def test_noalloc_with_one_split_runs_the_unsplit_kernel(lib):
     torch.cuda.synchronize()
     check_against_oracle(c, a, bp, s, bias)
     assert np.isfinite(c.float().cpu().numpy()).all()
+
+
+def test_noalloc_replays_under_graph_capture(lib):
+    """A split noalloc call captured into a HIP graph (after an eager call on the device, as the header asks)
+    replays correctly: each replay, with new activations copied into the captured input and eager work on the
+    stream between replays, gives the bits of the eager feather_scaled_mm_splitk on the same inputs."""
+    m, n, k, tile, splits = 512, 2048, 2560, (2, 2, 4, 4, 4, 1), 4
+    a, bp, s, bias = _inputs(m, n, k, torch.float16, torch.float16, seed=40)
+    warm = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    assert _call(lib, lib.feather_scaled_mm_splitk_noalloc, a, bp, s, bias, warm, tile, splits)  # eager first
+    torch.cuda.synchronize()
+    need = lib.feather_splitk_workspace_bytes(m, n, k, *tile, splits)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    got = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            ok = _call(lib, lib.feather_scaled_mm_splitk_noalloc, a, bp, s, bias, got, tile, splits)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert ok
+    g = torch.Generator("cpu").manual_seed(41)
+    for replay in range(4):
+        print(f"noalloc graph replay {replay}", flush=True)
+        a.copy_(torch.randn(m, k, generator=g).to(torch.float16).cuda())
+        want = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        assert _call(lib, lib.feather_scaled_mm_splitk, a, bp, s, bias, want, tile, splits, ws.data_ptr(), need)
+        torch.cuda.synchronize()
+        got.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), replay
+    check_against_oracle(got, a, bp, s, bias, rows=sample_rows(m, n_random=8))
