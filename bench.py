@@ -40,13 +40,104 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 
 # HBM bytes per launch, by (cell, tile): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of `bench.py --only <cell>`
 # (KiB per dispatch), scaled by the factors a 512 MiB device-to-device copy gives the same counters
-# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000). Re-measure when the kernel changes; a tile without a
-# measurement reports null.
-MEASURED_TRAFFIC_BYTES = {
-    ("c3", (2, 2, 4, 4, 8, 1)): (184487 * 2.0 + 98304 * 1.0) * 1024,
-    ("c3", (1, 4, 4, 8, 4, 1)): (185289 * 2.0 + 98304 * 1.0) * 1024,
-    ("c4", (8, 1, 4, 1, 4, 0)): (29218 * 2.0 + 448 * 1.0) * 1024,
-}
+# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000), measured on the kernel sources whose digest is
+# TRAFFIC_SOURCES_SHA16 (`kernel_sources_sha16()`). A run whose sources differ, or a tile without a
+# measurement, reports traffic null: the figure belongs to the build it was measured on.
+TRAFFIC_SOURCES_SHA16 = None
+MEASURED_TRAFFIC_BYTES = {}
+KERNEL_SOURCES = ("csrc/scaled_mm_kernels.h", "csrc/scaled_mm_launch.hip", "csrc/scaled_mm_launch.h",
+                  "csrc/feather_tiles.h", "csrc/scaled_mm_api.hip")
+
+
+def kernel_sources_sha16() -> str:
+    """First 16 hex digits of the SHA-256 over the matmul kernels' sources (names and contents, in order)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update(rel.encode())
+        h.update((ROOT / "feather-ops_amd" / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(cell: str, tile) -> float | None:
+    """HBM bytes per launch of `cell` on `tile` if they were measured on these kernel sources, else None."""
+    if TRAFFIC_SOURCES_SHA16 is None or kernel_sources_sha16() != TRAFFIC_SOURCES_SHA16:
+        return None
+    return MEASURED_TRAFFIC_BYTES.get((cell, tuple(tile)))
+
+
+class ClockMonitor:
+    """The GPU's shader clock while a load runs: a thread reads the SMU's metrics table (amdsmi
+    `gpu_metrics`: current GFX clock of every XCD) every `period_s` between start() and stop(). The table
+    is the power management's own view, refreshed every few milliseconds; a clock read between kernels
+    instead (a few microseconds after the MFMA load stops) already shows it recovering toward 2.4 GHz, so
+    the sampling has to run during the load. Unavailable (amdsmi missing, no matching device): samples
+    stay empty and summary() returns None."""
+
+    def __init__(self, period_s: float = 0.002):
+        import threading
+
+        self.period_s = period_s
+        self.samples = []
+        self._stop = threading.Event()
+        self._thread = None
+        self._handle = None
+        self._amdsmi = None
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            if len(handles) == 1:
+                self._handle = handles[0]
+                self._amdsmi = amdsmi
+        except Exception:  # amdsmi absent or refused: no clock figure, the benchmark itself is unaffected
+            self._amdsmi = None
+
+    def _read(self):
+        metrics = self._amdsmi.amdsmi_get_gpu_metrics_info(self._handle)
+        clks = [c for c in (metrics.get("current_gfxclks") or []) if isinstance(c, int) and 0 < c < 10000]
+        return clks
+
+    def _run(self):
+        import time as _time
+
+        while not self._stop.is_set():
+            try:
+                clks = self._read()
+            except Exception:
+                return
+            if clks:
+                self.samples.append((_time.perf_counter(), clks))
+            self._stop.wait(self.period_s)
+
+    def start(self):
+        import threading
+
+        if self._amdsmi is not None:
+            self._stop.clear()
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+
+    def stop(self):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+            self._thread = None
+
+    def summary(self) -> dict | None:
+        """Median over the samples of the mean XCD clock, its p10/p90, and each XCD's median; None without samples."""
+        if not self.samples:
+            return None
+        means = [sum(c) / len(c) for _, c in self.samples]
+        n_xcd = min(len(c) for _, c in self.samples)
+        per_xcd = [_percentile([c[i] for _, c in self.samples], 0.5) for i in range(n_xcd)]
+        return {"clock_mhz": round(_percentile(means, 0.5), 1), "p10_mhz": round(_percentile(means, 0.1), 1),
+                "p90_mhz": round(_percentile(means, 0.9), 1), "per_xcd_mhz": [round(v, 1) for v in per_xcd],
+                "samples": len(means),
+                "method": "amdsmi gpu_metrics current_gfxclks (every XCD), sampled every 2 ms by a thread during "
+                          "the timed rounds"}
 
 
 def algorithmic_bytes(m: int, k: int, n: int, bias: bool = False) -> int:
@@ -87,14 +178,14 @@ def _percentile(values, q):
 
 
 def steady_rounds(launch_round, launches: int, rounds: int, warmup: int, min_warm_s: float = 1.0,
-                  max_warm_s: float = 6.0, tol: float = 0.02) -> dict:
+                  max_warm_s: float = 6.0, tol: float = 0.02, monitor: "ClockMonitor | None" = None) -> dict:
     """Time `launch_round` (enqueues `launches` kernel launches on the current stream) at steady state.
 
     `warmup` untimed launches' worth of rounds first, then more rounds until the clocks settle (at least
     min_warm_s of continuous work and the last three round times within `tol` of each other; at most
     max_warm_s), then `rounds` timed rounds. Each round is bracketed by device synchronisation and timed
     with HIP events on the launching stream. Returns microseconds per launch: median, p20, p80, plus the
-    warm-up actually run.
+    warm-up actually run. A `monitor` (ClockMonitor) samples the clock during the timed rounds only.
     """
     import torch
 
@@ -119,7 +210,11 @@ def steady_rounds(launch_round, launches: int, rounds: int, warmup: int, min_war
             break
         warm.append(one())
     warm_s = time.perf_counter() - t0
+    if monitor is not None:
+        monitor.start()
     timed = [one() for _ in range(rounds)]
+    if monitor is not None:
+        monitor.stop()
     return {"us": _percentile(timed, 0.5), "p20_us": _percentile(timed, 0.2), "p80_us": _percentile(timed, 0.8),
             "rounds": rounds, "launches_per_round": launches, "warmup_launches": len(warm) * launches,
             "warmup_s": round(warm_s, 2), "last_warmup_us": warm[-1]}
@@ -146,10 +241,12 @@ def time_c3(steps: int, warmup: int, rounds: int):
         for _ in range(steps):
             op(a, b, s, None, out, *tile)
 
-    t = steady_rounds(launch_round, steps, rounds, warmup)
+    monitor = ClockMonitor()
+    t = steady_rounds(launch_round, steps, rounds, warmup, monitor=monitor)
+    clock = monitor.summary()
     flops = 2.0 * m * n * k
     return {"m": m, "k": k, "n": n, "tile": list(tile), "t": t, "tflops": flops / (t["us"] * 1e-6) / 1e12,
-            "bytes": algorithmic_bytes(m, k, n)}
+            "bytes": algorithmic_bytes(m, k, n), "clock": clock}
 
 
 def time_square_cell(m: int, k: int, n: int, a_fmt: str, fp8: str, steps: int, warmup: int, rounds: int):
@@ -392,6 +489,9 @@ def main() -> int:
     sec = not args.no_secondary
     c4 = time_c4(rounds) if sec else None
     c2 = time_square_cell(4096, 3072, 3072, "bf16", "e5m2", 50, 10, rounds) if sec else None
+    # the same shape with fp16 activations: separates the bf16 widening's cost from the grid's (one round of
+    # 768 128 x 128 blocks)
+    c2h = time_square_cell(4096, 3072, 3072, "fp16", "e5m2", 50, 10, rounds) if sec else None
     e4 = time_square_cell(4096, 3072, 12288, "fp16", "e4m3fn", 20, 10, rounds) if sec else None
     bw = time_bf16_auto_cell(4096, 3072, 12288, 20, 10, rounds) if sec else None
     # 168 tiles of 128 x 128 for 256 CUs; the unsplit control is the best unsplit tile of the sweep
@@ -411,6 +511,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(t3["us"] * 1e-3, 5),
+        "clock_mhz": c3["clock"]["clock_mhz"] if c3["clock"] else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -428,8 +529,14 @@ def main() -> int:
                                   "(at most 6 s)"},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(c3["tflops"] / PEAK_FP16_TFLOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES.get(("c3", tuple(c3["tile"])))},
+                     "traffic": measured_traffic("c3", c3["tile"]),
+                     "traffic_sources_sha16": TRAFFIC_SOURCES_SHA16},
+        "kernel_sources_sha16": kernel_sources_sha16(),
     }
+    if c3["clock"]:
+        line["clock"] = {**c3["clock"], "peak_assumes_mhz": 2400,
+                         "frac_at_measured_clock": round(c3["tflops"] / (PEAK_FP16_TFLOPS * c3["clock"]["clock_mhz"]
+                                                                         / 2400.0), 4)}
     if c4 is not None:
         t4 = c4["t"]
         line["hbm_cell"] = {"workload": "C4 skinny: fp16 [16,4096] x e5m2 [14336,4096] -> fp16",
@@ -439,10 +546,15 @@ def main() -> int:
                             "algorithmic_bytes": c4["bytes"], "weight_copies_rotated": c4["weight_copies"],
                             "timed_as": f"HIP graph of 32 launches, {t4['launches_per_round'] // 32} replays per round, "
                                         f"median of {t4['rounds']} rounds (launch gaps included)",
-                            "traffic": MEASURED_TRAFFIC_BYTES.get(("c4", tuple(c4["tile"])))}
+                            "traffic": measured_traffic("c4", c4["tile"])}
     if c2 is not None:
         line["bf16_cell"] = {"workload": "C2 DiT attention projection: bf16 [4096,3072] x e5m2 [3072,3072] -> bf16",
                              **c2, "frac_fp16_peak": round(c2["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
+        if c2h is not None:
+            line["bf16_cell"]["fp16_activations"] = {
+                "workload": "the same shape with fp16 activations and output", **c2h,
+                "frac_fp16_peak": round(c2h["TFLOPs"] / PEAK_FP16_TFLOPS, 4),
+                "bf16_over_fp16_time": round(c2["us_per_launch"] / c2h["us_per_launch"], 4)}
     if e4 is not None:
         line["e4m3_cell"] = {"workload": "C3 shape with e4m3fn weights: fp16 [4096,3072] x e4m3fn [12288,3072] -> fp16",
                              **e4, "frac_fp16_peak": round(e4["TFLOPs"] / PEAK_FP16_TFLOPS, 4)}
