@@ -1087,7 +1087,11 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
         u32x4 b[S::kGroups][RN];
     };
     // One iteration's operands: activations into LDS buffer `buf`, weights into registers. The LDS wait
-    // first retires this wave's reads of the buffer being refilled.
+    // first retires this wave's reads of the buffer being refilled. Branch-free (chunks past the range take
+    // the out-of-range offset, also for whole iterations past the end, which then load zeros and move no
+    // data): every path through the main loop then has the same loads in flight, so the compiler's own
+    // register waits agree with the explicit ones below. (With a branch here and a conditional last fetch,
+    // the merged paths made it wait for the fetch just issued, one iteration of lead instead of two.)
     auto fetch = [&](Frag& f, int buf, int it) {
         __builtin_amdgcn_s_waitcnt(kLgkm0Imm);
 #pragma unroll
@@ -1095,21 +1099,13 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             const int group = group0 + (it * S::kGroups + q) * KS + ks;   // K slices interleave group by group
             const uint32_t a_soff = static_cast<uint32_t>(group) * 128u;
             uint8_t* const dst = a_lds + buf * S::kABufBytes + q * RM * S::kAFragBytes;
-            if (4 * group + 3 < chunk_end) {
 #pragma unroll
-                for (int i = 0; i < RM; ++i)
+            for (int i = 0; i < RM; ++i)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, a_dma[i][h], a_soff);
-            } else {
-#pragma unroll
-                for (int i = 0; i < RM; ++i)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const bool ok = 4 * group + a_dma_chunk[h] < chunk_end;
-                        dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, ok ? a_dma[i][h] : kOob, a_soff);
-                    }
-            }
+                for (int h = 0; h < 2; ++h) {
+                    const bool ok = 4 * group + a_dma_chunk[h] < chunk_end;
+                    dma16(a_rsrc, dst + i * S::kAFragBytes + h * 1024, ok ? a_dma[i][h] : kOob, a_soff);
+                }
             const int chunk = 4 * group + g;
             const bool in_k = chunk < chunk_end;
 #pragma unroll
@@ -1157,25 +1153,30 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
 
     // Iterations of this wave: groups ks, ks + KS, ... taken kGroups at a time; fetch it + 1 is in flight
     // while iteration it computes. Before a consume, this wave's loads of that iteration have landed
-    // (vector-memory operations retire in issue order, so only the newer fetch may stay outstanding).
+    // (vector-memory operations retire in issue order, so only the newer fetch may stay outstanding). The
+    // loop body is straight-line: its second fetch goes out even in the last pair of iterations, where it
+    // loads zeros that are never consumed.
+    // Scheduling barriers keep each fetch ahead of the decode of the iteration before it (left alone, the
+    // compiler hoists that decode above the fetch, and its register wait then retires the older fetch before
+    // the newer one is issued).
     const int per_iter = S::kGroups * KS;
     const int iters = (group_end - group0 + per_iter - 1) / per_iter;
     Frag f0, f1;
-    if (iters > 0) fetch(f0, 0, 0);
+    fetch(f0, 0, 0);
     int it = 0;
     for (; it + 1 < iters; it += 2) {
+        __builtin_amdgcn_sched_barrier(0);
         fetch(f1, 1, it + 1);
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
         consume(f0, 0);
-        if (it + 2 < iters) {
-            fetch(f0, 0, it + 2);
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
-        } else {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(f0, 0, it + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
         consume(f1, 1);
     }
-    if (it < iters) {
+    if (it < iters) {  // an odd count: the last fetch is a real one
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         consume(f0, 0);
     }
