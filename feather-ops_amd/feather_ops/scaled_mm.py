@@ -38,6 +38,11 @@ _TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
 _TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
 _TILE_STREAM_32x64 = (2, 2, 4, 2, 2, 0)
 _TILE_STREAM_16x64 = (8, 1, 4, 1, 4, 0)
+# The same 16 x 64 block with 4 K slices (4 waves), and a 16 x 32 block with 8: with two fetches in flight per
+# wave (16 KiB of weight per wave at 64 columns), 4 slices keep ~32 KiB per CU in flight where 8 keep ~64 KiB,
+# which oversubscribes HBM on weights of 50-100 MB (C4: 11.86 against 12.14 us, graph-timed, cold weights).
+_TILE_STREAM_16x64_KS4 = (4, 1, 4, 1, 4, 0)
+_TILE_STREAM_16x32 = (8, 1, 4, 1, 2, 0)
 
 # MI355X: 256 compute units.
 _CUS = 256
@@ -90,20 +95,44 @@ _SMALL_GRID_MAX_SPLITS = {_TILE_RING_64x128: 3, _TILE_RING_128x128: 4}
 # Partial sums of one split launch stay within the allocation-free entry point's static array.
 _SPLIT_MAX_PARTIAL_BYTES = 64 << 20
 
-# 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more (1.5 times that
-# for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on, the 64 x 64 tile below, split to
-# about _MID_M_RING_BLOCKS workgroups.
-_MID_M_RING_MIN_WEIGHT = 1 << 26
-_MID_M_WIDE_TILES = 320
+# 16 < M <= 64: the 64-row ring tiles once the weight has _MID_M_RING_MIN_WEIGHT bytes or more for 32 < M <= 64
+# (_MID_M_RING_MIN_WEIGHT_32 for M <= 32): the 64 x 128 tile from _MID_M_WIDE_TILES of its tiles on (where the
+# 64 x 64 tile would have more tiles than CUs: 1.03-1.3x over it on 24 such cells, fp16 and bf16), the 64 x 64
+# tile below (1.0-1.4x over the 64 x 128 tile on 22 of 28 cells), split by `_mid_m_ring_splits`; the split
+# count of the 64 x 128 tile there was about _MID_M_RING_BLOCKS workgroups before (it still is for M <= 32 at
+# LM-head widths). For 32 < M <= 64 the 16-row streaming tiles, which
+# read the weight once per 16 rows, lose 4-29% to the split ring tiles from 40 MB on (held-out cells at M 40-64
+# and weights of 32-58 MB) and win below it (6144 x 6144, 8192 x 4096 at M <= 48).
+_MID_M_RING_MIN_WEIGHT = 40 << 20
+_MID_M_RING_MIN_WEIGHT_32 = 96 << 20
+_MID_M_WIDE_TILES = 129
 _MID_M_RING_BLOCKS = 512
+# The 64-row ring tiles' split count (`_mid_m_ring_splits`): workgroups per CU it considers (the 64 x 64 tile's
+# deep ring holds 4; the 64 x 128 tile measured best at up to 3), the rate of a block alone on its CU, and the
+# fixed cost of one split as a fraction of a tile's time.
+_MID_M_MAX_PER_CU = {_TILE_RING_64x64: 4, _TILE_RING_64x128: 3}
+_MID_M_LONE_RATE = 0.6
+# bf16 activations on the 64 x 128 tile (register-staged ring): the rate at 1, 2, 3 and 4 workgroups per CU; it
+# wants 3-4 per CU (best measured splits 544-960 workgroups on 12 cells, against 408-480 with fp16)
+_MID_M_STAGED_RATES = (0.6, 0.75, 0.9, 1.0)
+_MID_M_SPLIT_COST = 0.04
 
-# The 16 x 64 streaming tile splits K from this K when it has fewer than _STREAM_SPLIT_MAX_TILES tiles (the
-# 3 splits of more than 128 tiles fit two workgroups per CU up to 170 tiles; at 176 the unsplit tile wins),
-# aiming at _STREAM_SPLIT_BLOCKS workgroups with at least _STREAM_SPLIT_MIN_RANGE of K each.
+# Skinny M with a long K and a narrow weight (K >= _STREAM_SPLIT_MIN_K, fewer than _STREAM_SPLIT_MAX_TILES tiles of
+# 16 x 64): a streaming tile split along K (`_stream_split`). For M <= _STREAM_TINY_M the 16 x 32 tile (few
+# activation rows for every block to re-read, and narrower blocks give more of them), else the 16 x 64 tile with 4 K slices
+# (its activations, re-read by every block, are amortized over twice the columns); the most splits of
+# _STREAM_SPLIT_COUNTS that keep the workgroups within one per CU and each K range at least
+# _STREAM_SPLIT_MIN_RANGE deep; and no split when that
+# leaves _STREAM_SPLIT_MIN_WORKGROUPS or fewer workgroups (the unsplit rule's narrower tiles then do better).
+# With one row of tiles, workgroup counts just past the CU count lose 10-25% (some CUs run two), hence the
+# one-per-CU cap; each further row of tiles raises it by _STREAM_SPLIT_CAP_PER_ROW.
 _STREAM_SPLIT_MIN_K = 8192
 _STREAM_SPLIT_MAX_TILES = 171
-_STREAM_SPLIT_BLOCKS = 192
-_STREAM_SPLIT_MIN_RANGE = 2048
+_STREAM_TINY_M = 12
+_STREAM_SPLIT_COUNTS = (8, 6, 4, 3, 2)
+_STREAM_SPLIT_MIN_RANGE = 3072
+_STREAM_SPLIT_MIN_WORKGROUPS = 128
+_STREAM_SPLIT_CAP_PER_ROW = 64
 
 # bf16 activations: the auto path widens them once up front (feather_ops::widen_bf16, the kernels' own
 # round-to-nearest-even conversion, so the result is the same bits) and runs the fp16-activation kernel when
@@ -140,6 +169,48 @@ def _stream_reread(M: int, N: int, K: int) -> float:
     slots its blocks fill in their last round."""
     blocks = _blocks(M, N, _TILE_STREAM_16x64)
     return -(-M // 16) * N * K * (_CUS * -(-blocks // _CUS)) / blocks
+
+
+def _stream_split(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int, int], int] | None:
+    """(tile, splits) for the long-K streaming regime, or None where the unsplit streaming rule applies (see
+    _STREAM_SPLIT_MIN_K above). Measured with the tile sweep on 48 decoder-shaped cells (M 1-32, N 2048-28672,
+    K 3072-28672) and the grid's skinny cells, fp16 and bf16, graph-timed with cold weights."""
+    tiny = M <= _STREAM_TINY_M
+    tile = _TILE_STREAM_16x32 if tiny else _TILE_STREAM_16x64_KS4
+    tiles = _blocks(M, N, tile)
+    # more row tiles share each weight panel (its second read hits the caches), and tolerate a few more
+    # workgroups than CUs: 32 x 5120 x 13824 runs 1.27x faster split 2 ways (320 workgroups) than unsplit
+    cap = _CUS + _STREAM_SPLIT_CAP_PER_ROW * (-(-M // 16) - 1)
+    for splits in _STREAM_SPLIT_COUNTS:
+        if tiles * splits <= cap and K // splits >= _STREAM_SPLIT_MIN_RANGE:
+            if tiles * splits > _STREAM_SPLIT_MIN_WORKGROUPS or tiles * splits > _stream_unsplit_shape(M, N)[1]:
+                return tile, splits
+            return None
+    # no split within the cap: from 129 tiles of 16 x 64 on, that tile split 3 ways (two workgroups on most CUs)
+    # still beats the unsplit tile for M > 4 (12 x 10240 x 16384, 160 tiles: 1.03x; M <= 2: 0.96x); at 176 tiles
+    # it no longer does (above the regime's tile limit)
+    if M > 4 and _blocks(M, N, _TILE_STREAM_16x64_KS4) > 128 and K // 3 >= _STREAM_SPLIT_MIN_RANGE:
+        return _TILE_STREAM_16x64_KS4, 3
+    return None
+
+
+def _stream_unsplit_shape(M: int, N: int) -> tuple[int, int]:
+    """(repeat_n, blocks) of the unsplit 16-row streaming tile `select_scaled_mm_config` falls back to: as wide
+    as still gives 160 blocks (64, 32 or 16 columns)."""
+    rows = -(-M // 16)
+    for repeat_n in (4, 2, 1):
+        if rows * (N // (16 * repeat_n)) >= 160:
+            break
+    blocks = {rn: rows * -(-N // (16 * rn)) for rn in (4, 2, 1)}
+    if rows == 1 and _CUS < blocks[repeat_n] <= _CUS * 3 // 2:
+        # one row of blocks and a small second round (some CUs run two blocks, most one): a width that keeps
+        # within one round (at least 128 blocks) or spreads over more than 1.5 rounds does better (1 x 17408 x
+        # 18432 on 32 columns: 1.08x; 16 x 21504 x 4096: 1.04x; 1 x 4608 x 12288 on 32 columns, 144 blocks
+        # against 288 of 16 columns: 1.45x)
+        fits = [rn for rn in (4, 2, 1) if _CUS // 2 <= blocks[rn] <= _CUS]
+        spread = [rn for rn in (4, 2, 1) if blocks[rn] > _CUS * 3 // 2]
+        repeat_n = (fits or spread or [repeat_n])[0]
+    return repeat_n, blocks[repeat_n]
 
 
 def _small_grid_time(M: int, N: int, K: int, tile: tuple[int, ...], splits: int, a_bf16: bool) -> float:
@@ -221,17 +292,21 @@ def select_scaled_mm_config(
       bf16 ones stream faster there); else streaming.
     - 16 < M <= 64 with a big weight: the 64-row ring tiles, which read the weight once where the 16-row
       streaming tiles read it once per 16 rows (on small grids they run their deep-ring variant): from a
-      64 MB weight (N * K bytes; 96 MB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
+      40 MiB weight (N * K bytes; 96 MiB when M <= 32) the 64 x 128 tile from 320 of its tiles on, else
       the 64 x 64 tile, split along K to fill the CUs (`select_scaled_mm_splits`); for 16 < M <= 32 also
       the 64 x 128 tile from 512 of its tiles on.
     - M <= 16 with 512 to 1024 64 x 128 tiles (N from 65536 to 131072, LM-head widths): that ring tile,
       whose direct-to-LDS weight stream runs 5-12% faster than the streaming tiles there; beyond 1024
       tiles the second, partial wave of blocks makes it slower.
     - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
-    - K >= 8192 with at most 170 16 x 64 streaming tiles: that tile (8 K slices per block), split along
-      K across workgroups (`select_scaled_mm_splits`).
+    - K >= 8192 with at most 170 16 x 64 streaming tiles: the 16 x 32 tile (8 K slices) for M <= 12, the
+      16 x 64 tile (4 K slices) above, split along K to at most one workgroup per CU
+      (`select_scaled_mm_splits`), where that gives more workgroups than the unsplit rule below.
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
-      columns), with 8 K slices per block up to one block per CU, 4 beyond (two blocks share a CU).
+      columns): 16 x 64 with 4 K slices, the narrower ones with 8 up to one block per CU and 4 beyond.
+    The streaming picks were refitted after the streaming kernel's loop kept two fetches in flight per wave
+    (it had been one): on 193 swept cells with M <= 256 the picks are at 0.994 of the best candidate in
+    geometric mean, against 0.953 for the rules before.
     """
     del b_dtype, out_dtype
     a_bf16 = a_dtype == torch.bfloat16
@@ -246,7 +321,7 @@ def select_scaled_mm_config(
         return _small_grid_choice(M, N, K, a_bf16)[0]
     if M > 64 and _blocks(M, N, _TILE_RING_64x64) >= 2 * _CUS:
         return _TILE_RING_64x64
-    if 16 < M <= 64 and N * K >= _MID_M_RING_MIN_WEIGHT * (2 if M > 32 else 3) // 2:
+    if 16 < M <= 64 and N * K >= (_MID_M_RING_MIN_WEIGHT if M > 32 else _MID_M_RING_MIN_WEIGHT_32):
         wide = _blocks(M, N, _TILE_RING_64x128) >= _MID_M_WIDE_TILES
         return _TILE_RING_64x128 if wide else _TILE_RING_64x64
     if M <= 32:
@@ -256,15 +331,15 @@ def select_scaled_mm_config(
     if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) > 3 * _CUS // 2:
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
-        return _TILE_STREAM_16x64
+        split = _stream_split(M, N, K)
+        if split is not None:
+            return split[0]
     if M > 768 and not a_bf16 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
         return _TILE_RING_64x64
-    rows = -(-M // 16)
-    for repeat_n in (4, 2, 1):
-        if rows * (N // (16 * repeat_n)) >= 160:
-            break
-    blocks = rows * -(-N // (16 * repeat_n))
-    return (8 if blocks <= _CUS else 4, 1, 4, 1, repeat_n, 0)
+    repeat_n, blocks = _stream_unsplit_shape(M, N)
+    # 8 K slices while the blocks fit one per CU, 4 beyond; the 64-column tile takes 4 either way (its 8-slice
+    # form keeps twice the weight in flight, past what the HBM serves best: C4 2.5% slower with it)
+    return (8 if blocks <= _CUS and repeat_n < 4 else 4, 1, 4, 1, repeat_n, 0)
 
 
 def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
@@ -285,21 +360,28 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
       1000 x 1000 x 2560 and 1024 x 1024 x 3072 (256 tiles): 2 splits, 394 and 453 TFLOP/s against 329
       and 358 unsplit.
     - K >= 8192 with at most 170 16 x 64 streaming tiles (skinny M, narrow N, long K: a decoder's down
-      projection): that tile splits into about 192 workgroups (at most 128 tiles; 2 to 8 splits, each at
-      least 2048 deep), or 3 ways from 129 to 170 tiles, so the blocks come close to whole multiples of
-      the CU count without passing two per CU (16 x 11264 x 11264, 176 tiles: 160 TFLOP/s unsplit
-      against 132 split 3 ways). Measured (HIP-graph replays, cold weights) 15-45% faster than the best unsplit tile on
-      twelve such cells, within 4% of the best split count on most; at 224 tiles (16 x 14336 x 16384) the
-      unsplit tile is faster.
-    - 16 < M <= 64 on a 64-row ring tile: about 512 workgroups, 1 to 8 splits of at least 16 stages. At
-      so few rows the ring is latency-bound, and more workgroups keep more of the weight in flight:
-      64 x 16384 x 4096 414 TFLOP/s on the 64 x 64 tile split 2 ways against 360 unsplit; 64 x 5120 x
-      13824 379 split 6 ways against 130 (and 262 for the best streaming tile).
+      projection), on the streaming tile `select_scaled_mm_config` picks there (`_stream_split`): the most of
+      8, 6, 4, 3, 2 splits that keep the workgroups within one per CU (plus 64 per further row of 16-row
+      tiles) and every K range at least 3072 deep, where that gives more than 128 workgroups or more than the
+      unsplit rule would; else 3 splits of the 16 x 64 tile from 129 of its tiles on when M > 4. Workgroup
+      counts just past the CU count lose 10-25% (1 x 5120 x 13824 on 16 x 32: 160 workgroups 1.0, 320 0.75,
+      480 0.90); 2 x 4096 x 16384 runs 1.05x faster split 2 ways on 16 x 32 than split 3 ways on the
+      8-slice 16 x 64 tile the rule before took, 16 x 2048 x 8192 1.27x faster on the unsplit 16 x 16 tile.
+    - 16 < M <= 64 on the 64 x 64 ring tile: the split count of a residency model (`_mid_m_ring_splits`,
+      1 to 8 splits of at least 16 stages), which matches the measured best on every such cell of the
+      sweeps: 64 x 16384 x 4096 2 splits (414 TFLOP/s against 360 unsplit), 64 x 5120 x 13824 6 (379 against
+      130), 32 x 11264 x 11264 4 (1.18x the 2 of the ~512-workgroup rule before). On the 64 x 128 tile:
+      about 512 workgroups, one split less when the last round would fill under a quarter of the CUs.
     Shorter K loses: the per-split fixed costs (pipeline fill, the partial sums' round trip through
     memory, the workspace lookup on the host) dominate.
     """
     tile = tuple(tile)
-    if tile in (_TILE_RING_64x128, _TILE_RING_64x64) and 16 < M <= 64:
+    big_weight = N * K >= (_MID_M_RING_MIN_WEIGHT if M > 32 else _MID_M_RING_MIN_WEIGHT_32)
+    if tile in (_TILE_RING_64x64, _TILE_RING_64x128) and 16 < M <= 64 and big_weight:
+        if tile != select_scaled_mm_config(M, N, K, a_dtype):
+            return 1
+        return _mid_m_ring_splits(M, N, K, tile, a_dtype == torch.bfloat16)
+    if tile == _TILE_RING_64x128 and 16 < M <= 64:
         if tile != select_scaled_mm_config(M, N, K, a_dtype):
             return 1
         tiles = _blocks(M, N, tile)
@@ -309,12 +391,13 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
         if splits > 1 and 0 < (tiles * splits) % _CUS < _CUS // 4:
             splits -= 1
         return splits
-    if tile == _TILE_STREAM_16x64 and K >= _STREAM_SPLIT_MIN_K:
-        tiles = _blocks(M, N, tile)
-        if tile != select_scaled_mm_config(M, N, K, a_dtype) or tiles >= _STREAM_SPLIT_MAX_TILES:
+    if tile in (_TILE_STREAM_16x32, _TILE_STREAM_16x64_KS4) and K >= _STREAM_SPLIT_MIN_K:
+        if _blocks(M, N, _TILE_STREAM_16x64) >= _STREAM_SPLIT_MAX_TILES:
             return 1
-        aim = round(_STREAM_SPLIT_BLOCKS / tiles) if tiles <= _CUS // 2 else 3
-        return max(2, min(8, aim, K // _STREAM_SPLIT_MIN_RANGE))
+        split = _stream_split(M, N, K)
+        if split is None or split[0] != tile or tile != select_scaled_mm_config(M, N, K, a_dtype):
+            return 1
+        return split[1]
     if tile == _TILE_RING_64x64 and M > 768:
         return _ring_splits(M, N, K, tile)[0] if tile == select_scaled_mm_config(M, N, K, a_dtype) else 1
     if M <= 64 or K < _SPLIT_MIN_K or tile not in (_TILE_RING_128x128, _TILE_RING_64x128):
@@ -328,6 +411,30 @@ def select_scaled_mm_splits(M: int, N: int, K: int, tile: tuple[int, ...],
         return _small_grid_choice(M, N, K, a_dtype == torch.bfloat16)[1]
     wide_bf16 = a_dtype == torch.bfloat16 and tile == _TILE_RING_64x128
     return _ring_splits(M, N, K, tile, least=2, per_cu=3 if wide_bf16 else 2)[0]
+
+
+def _mid_m_ring_splits(M: int, N: int, K: int, tile: tuple[int, ...] = _TILE_RING_64x64,
+                       a_bf16: bool = False) -> int:
+    """Splits of a 64-row ring tile for 16 < M <= 64 and a big weight: the count with the least modelled time,
+    where the busiest CU runs ceil(workgroups / CUs) workgroups of 1 / splits of a tile each (all resident at
+    once, up to _MID_M_MAX_PER_CU per CU), a block alone on its CU at _MID_M_LONE_RATE of the rate,
+    and each split costs _MID_M_SPLIT_COST of a tile's time; counts of _STREAM_SPLIT_COUNTS (the measured
+    ones), at least 16 stages of 64 per split. It matches the
+    best measured count on every mid-M cell of the sweeps (e.g. 176 tiles: 4 splits, 1.18x faster than the 2 of
+    the ~512-workgroup rule it replaced; 80 tiles: 6; 224 tiles: 2)."""
+    tiles = _blocks(M, N, tile)
+    staged = a_bf16 and tile == _TILE_RING_64x128   # bf16 on its 4 column waves: the register-staged ring
+    rates = _MID_M_STAGED_RATES if staged else (_MID_M_LONE_RATE,) + (1.0,) * 3
+    best = (float("inf"), 1)
+    for splits in (1,) + _STREAM_SPLIT_COUNTS[::-1]:
+        if splits > 1 and -(-K // 64) // splits < _SPLIT_MIN_STAGES:
+            break
+        per_cu = -(-tiles * splits // _CUS)
+        if per_cu > (4 if staged else _MID_M_MAX_PER_CU[tile]):
+            break
+        time = per_cu / splits / rates[per_cu - 1] + _MID_M_SPLIT_COST * splits
+        best = min(best, (time, splits))
+    return best[1]
 
 
 def _ring_splits(M: int, N: int, K: int, tile: tuple[int, ...], least: int = 1,

@@ -293,35 +293,46 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(1040, 1536, 6144)[1] == 2                          # fp16: two per CU at most
     assert auto(4096, 12288, 3072) == ((1, 4, 4, 8, 4, 1), 1)   # full grids never split
     assert auto(16, 14336, 4096)[1] == 1
-    # skinny M, long K, fewer than 192 16 x 64 streaming tiles: that tile, split for about 192 workgroups
-    assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 4, 0), 3)      # 64 tiles
-    assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 4, 0), 3)
-    assert auto(1, 8192, 28672) == ((8, 1, 4, 1, 4, 0), 2)      # 128 tiles -> 256 workgroups
-    assert auto(16, 10240, 16384) == ((8, 1, 4, 1, 4, 0), 3)    # 160 tiles: 3 from 129 on
-    assert auto(16, 2048, 8192) == ((8, 1, 4, 1, 4, 0), 4)      # 32 tiles, but K ranges of 2048 at least
-    assert auto(1, 512, 65536) == ((8, 1, 4, 1, 4, 0), 8)       # at most 8
-    assert auto(16, 14336, 16384) == ((8, 1, 4, 1, 4, 0), 1)    # 224 tiles: unsplit
-    assert auto(16, 11264, 11264) == ((8, 1, 4, 1, 4, 0), 1)    # 176 tiles: 3 splits would pass 2 per CU
+    # skinny M, long K, fewer than 171 16 x 64 tiles: a streaming tile split to at most one workgroup per CU
+    # (the 16 x 32 tile for M <= 12, the 16 x 64 tile with 4 K slices above), each K range 3072 deep or more
+    assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 2, 0), 2)      # 128 tiles of 16 x 32 -> 256 workgroups
+    assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 2, 0), 2)
+    assert auto(1, 8192, 28672) == ((8, 1, 4, 1, 2, 0), 1)      # 256 tiles of 16 x 32: no split needed
+    assert auto(16, 4096, 16384) == ((4, 1, 4, 1, 4, 0), 4)     # 64 tiles of 16 x 64 -> 256 workgroups
+    assert auto(16, 5120, 13824) == ((4, 1, 4, 1, 4, 0), 3)     # 80 tiles -> 240
+    assert auto(32, 5120, 13824) == ((4, 1, 4, 1, 4, 0), 2)     # two rows of tiles: up to 320 workgroups
+    assert auto(16, 10240, 16384) == ((4, 1, 4, 1, 4, 0), 3)    # 160 tiles: 3 from 129 on
+    assert auto(1, 10240, 16384) == ((4, 1, 4, 1, 4, 0), 1)     # ... but not for M <= 4
+    assert auto(16, 2048, 8192) == ((8, 1, 4, 1, 1, 0), 1)      # 128 workgroups either way: unsplit 16 x 16
+    assert auto(1, 512, 65536) == ((8, 1, 4, 1, 2, 0), 8)       # at most 8; more workgroups than unsplit
+    assert auto(16, 14336, 16384) == ((4, 1, 4, 1, 4, 0), 1)    # 224 tiles: unsplit
+    assert auto(16, 11264, 11264) == ((4, 1, 4, 1, 4, 0), 1)    # 176 tiles: 3 splits would pass 2 per CU
     assert auto(8, 28672, 8192) == ((4, 1, 4, 1, 4, 0), 1)      # 448 tiles: a full grid, 4 slices, unsplit
     assert auto(16, 4096, 6144) == ((8, 1, 4, 1, 1, 0), 1)      # K < 8192: narrower tiles instead
     assert auto(32, 25600, 2048) == ((2, 2, 4, 2, 2, 0), 1)     # the 32-row tile's grid is full
-    # 32 < M <= 64 with a weight of 64 MB or more: the 64-row ring tiles, split to fill the CUs
+    # 32 < M <= 64 with a weight of 40 MB or more: the 64-row ring tiles (64 x 128 once 64 x 64 would have more
+    # tiles than CUs), split by the residency model
     assert auto(64, 16384, 4096) == ((2, 2, 4, 2, 2, 1), 2)     # 256 tiles of 64 x 64 -> 512 workgroups
-    assert auto(48, 32768, 4096) == ((2, 2, 4, 2, 2, 1), 1)     # 512 tiles
+    assert auto(64, 14336, 4096) == ((2, 2, 4, 2, 2, 1), 2)     # 58.7 MB: 224 tiles -> 448
+    assert auto(48, 12288, 4096) == ((2, 2, 4, 2, 2, 1), 4)     # 192 tiles -> 768, 3 per CU
+    assert auto(56, 11008, 4096) == ((2, 2, 4, 2, 2, 1), 4)     # 172 tiles -> 688
+    assert auto(64, 8192, 4096) == ((4, 1, 4, 1, 4, 0), 1)      # 32 MB: streaming
+    assert auto(52, 17408, 11264) == ((1, 4, 4, 4, 2, 1), 3)    # 272 tiles of 64 x 64: 136 of 64 x 128 -> 408
+    assert auto(48, 32768, 4096) == ((1, 4, 4, 4, 2, 1), 2)     # 256 tiles of 64 x 128 -> 512
     assert auto(64, 5120, 13824) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
     assert auto(64, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # 512 tiles of 64 x 128
     assert auto(48, 40960, 5120) == ((1, 4, 4, 4, 2, 1), 2)     # 320 tiles of 64 x 128
     assert auto(64, 65536, 1024) == ((1, 4, 4, 4, 2, 1), 1)
     assert auto(64, 16384, 2048) == ((4, 1, 4, 1, 4, 0), 1)     # 32 MB weight: streaming
-    assert auto(64, 8192, 4096) == ((4, 1, 4, 1, 4, 0), 1)
     assert auto(32, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # M <= 32: from a 96 MB weight
-    assert auto(32, 32768, 4096) == ((2, 2, 4, 2, 2, 1), 1)     # 512 tiles of 64 x 64
+    assert auto(32, 32768, 4096) == ((1, 4, 4, 4, 2, 1), 2)     # 256 tiles of 64 x 128
     assert auto(32, 5120, 25600) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
     assert auto(32, 16384, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 256 32-row tiles: the 16-row tile
     assert auto(40, 8448, 10496) == ((2, 2, 4, 2, 2, 1), 3)     # 132 tiles: 4 splits would leave 16 over
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1
-    assert splits(16, 14336, 16384, (8, 1, 4, 1, 4, 0)) == 1    # 224 tiles
+    assert splits(16, 14336, 16384, (4, 1, 4, 1, 4, 0)) == 1    # 224 tiles
+    assert splits(2, 4096, 16384, (4, 1, 4, 1, 4, 0)) == 1      # the heuristic picks 16 x 32 there
     for m in (65, 128, 200, 512, 1040, 2320):
         for n in (1024, 1536, 4096, 12288):
             for k in (4096, 6144, 16384):
@@ -352,7 +363,9 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     assert _auto_choice(512, 5120, 5120, bf) == ((2, 2, 4, 4, 4, 1), 3, False)    # split: in place
     assert _auto_choice(16, 14336, 4096, bf)[2] is False
     # M <= 64 on the 64 x 64 tile (the deep ring, which widens per fragment): big weights, split or not
-    assert _auto_choice(32, 25600, 5120, bf) == ((2, 2, 4, 2, 2, 1), 1, True)   # 1.19x measured
+    # (a big weight with more 64 x 64 tiles than CUs takes the 64 x 128 tile split in place instead, for bf16
+    # activations with more splits: 28 x 28672 x 25088 on it 1.13x over widened 64 x 64)
+    assert _auto_choice(32, 25600, 5120, bf) == ((1, 4, 4, 4, 2, 1), 4, False)
     assert _auto_choice(32, 5120, 25600, bf) == ((2, 2, 4, 2, 2, 1), 6, True)   # 1.16-1.17x
     assert _auto_choice(64, 16384, 4096, bf)[2] is False                         # 64 MB weight: 1.03x, kept
     assert _auto_choice(32, 14336, 4096, bf)[2] is False                         # streaming tile: 0.89x
@@ -406,8 +419,9 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(2304, 1280, 1280) == (2, 2, 4, 2, 2, 1)    # small grid, short K: 64 x 64 ring
     assert pick(512, 1024, 1024) == (4, 1, 4, 1, 4, 0)     # tiny grid: streaming, 4 K slices
     assert pick(32, 25600, 2048) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
-    assert pick(32, 25600, 5120) == (2, 2, 4, 2, 2, 1)     # ... and a 131 MB weight: the 64 x 64 ring tile
-    assert pick(16, 14336, 4096) == (8, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 8 K slices
+    assert pick(32, 25600, 5120) == (1, 4, 4, 4, 2, 1)     # ... and a 131 MB weight: the 64 x 128 ring tile
+    assert pick(32, 11264, 11264) == (2, 2, 4, 2, 2, 1)    # 127 MB, 176 64 x 64 tiles: that ring tile
+    assert pick(16, 14336, 4096) == (4, 1, 4, 1, 4, 0)     # C4: 224 blocks of 64 columns, 4 K slices
     assert pick(16, 4096, 4096) == (8, 1, 4, 1, 1, 0)      # narrow N: 16-column blocks for parallelism
     assert pick(16, 6144, 6144) == (8, 1, 4, 1, 2, 0)
     assert pick(1, 96768, 2688) == (1, 4, 4, 4, 2, 1)      # one row, LM-head width: 756 ring tiles

@@ -196,13 +196,16 @@ def test_ring_operand_schedules(fo, tile, n_tiles, splits, a_dtype):
 # wave-quantization choice among 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out
 # with a bias, against the oracle.
 HEURISTIC_CELLS = [
-    (2, 4096, 16384),    # 16 x 64 streaming tile split 3 ways along K across workgroups
+    (2, 4096, 16384),    # 16 x 32 streaming tile split 2 ways along K across workgroups
+    (16, 5120, 13824),   # 16 x 64 streaming tile, 4 slices, split 3 ways
+    (1, 17408, 4096),    # 16 x 32 columns: 64-column blocks would leave a small second round
     (16, 4096, 4096),    # 16 x 16 columns, 8 slices
     (16, 6144, 6144),    # 16 x 32 columns
     (32, 25600, 2048),   # 32-row streaming tile
     (32, 5120, 25600),   # 64 x 64 ring tile at 32 rows, split 6 ways along K (deep ring)
     (64, 16384, 4096),   # 64 x 64 ring tile at 64 rows (deep ring), split 2 ways along K
-    (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit
+    (52, 17408, 11264),  # 64 x 128 ring tile at 52 rows (more 64 x 64 tiles than CUs), split 3 ways
+    (24, 65536, 2048),   # 64 x 128 ring tile at 24 rows (512 tiles), unsplit (bf16: split 2 ways)
     (1, 96768, 2688),    # 64 x 128 ring tile at one row, an LM-head width (756 tiles)
     (128, 1024, 5120),   # 16-row tile, 8 row blocks
     (128, 4096, 14336),  # 64 x 128 ring tile split 8 ways (56 MiB weight, 32 tiles of 128 x 128)
@@ -271,13 +274,13 @@ def test_bf16_widened_first_replays_in_a_graph(fo):
         assert torch.equal(out.view(torch.int16), want.view(torch.int16))
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072), (32, 25600, 5120),
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (2320, 6144, 6144), (4096, 12288, 3072), (32, 11264, 11264),
                                    (32, 5120, 25600)])
 def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
     """Where the auto path widens bf16 activations first and runs the fp16-activation kernel, its output is the
     bits of the in-place widening on the same tile and split count (the C ABI's only bf16 form), bias and
-    per-column scale included: the 128 x 256 block and, at 32 rows, the 64 x 64 deep ring unsplit and split
-    6 ways."""
+    per-column scale included: the 128 x 256 block and, at 32 rows, the 64 x 64 deep ring split 4 and 6
+    ways."""
     from feather_ops.scaled_mm import _auto_choice
 
     tile, splits, widen = _auto_choice(m, n, k, torch.bfloat16)
