@@ -427,3 +427,30 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(1, 96768, 2688) == (1, 4, 4, 4, 2, 1)      # one row, LM-head width: 756 ring tiles
     assert pick(1, 151936, 3584) == (4, 1, 4, 1, 4, 0)     # 1187 ring tiles: a partial second wave
     assert pick(1, 32000, 4096) == (4, 1, 4, 1, 4, 0)      # 250 ring tiles: streaming
+
+
+def test_every_auto_launch_is_within_the_c_abi_contract(lib):
+    """Over seeded random shapes (M 1-20000, N a multiple of 8 up to 60000, K a multiple of 16 up to 40000) and
+    both activation dtypes, the auto path's (tile, splits) is a launch the C ABI accepts: an instantiated tile,
+    1 <= splits <= the tile's K units, a split workspace the library sizes (not -1) whose partial sums fit the
+    allocation-free entry point's static array, and splits only where the heuristic itself splits. The library
+    computes the workspace on the host, so no GPU call is made."""
+    import numpy as np
+
+    from feather_ops.scaled_mm import _auto_choice
+    from feather_ops.tiles import SCALED_MM_TILES, split_units
+
+    scratch = _header_scratch_bytes()
+    rng = np.random.default_rng(2026)
+    for _ in range(3000):
+        m = int(np.exp(rng.uniform(0, np.log(20000))))
+        n = int(rng.integers(1, 7501)) * 8
+        k = int(rng.integers(1, 2501)) * 16
+        for dt in (torch.float16, torch.bfloat16):
+            tile, splits, widen = _auto_choice(m, n, k, dt)
+            assert tile in SCALED_MM_TILES, (m, n, k, dt, tile)
+            assert 1 <= splits <= min(8, split_units(k, tile)), (m, n, k, dt, tile, splits)
+            if splits > 1:
+                ws = lib.feather_splitk_workspace_bytes(m, n, k, *tile[:5], bool(tile[5]), splits)
+                assert 0 < ws <= scratch, (m, n, k, dt, tile, splits, ws)
+            assert not widen or dt == torch.bfloat16
