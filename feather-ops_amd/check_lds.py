@@ -33,11 +33,11 @@ def _tiles():
 
 
 def expected_bytes(kernel: str, ints: list[int], bools: list[int] = ()) -> int:
-    """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`); a ring kernel's last template
-    flag is its deep-ring variant."""
+    """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`); a ring kernel's fifth template
+    flag is its deep-ring variant (the flags after it, such as non-temporal weight loads, leave LDS alone)."""
     if kernel == "ring_dma_kernel":
         warps_m, warps_n, unroll_k, repeat_m, repeat_n = ints
-        deep = bool(bools[-1]) if len(bools) == 5 else False
+        deep = bool(bools[4]) if len(bools) >= 5 else False
         slots_a, slots_b = _tiles().ring_slots((warps_m, warps_n, unroll_k, repeat_m, repeat_n, 1), deep)
         a_stage = 16 * warps_m * repeat_m * unroll_k * 32
         b_stage = 16 * warps_n * repeat_n * unroll_k * 16

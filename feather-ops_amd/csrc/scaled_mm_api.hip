@@ -4,7 +4,10 @@
 #include "feather_tiles.h"
 #include "scaled_mm_launch.h"
 
+#include <atomic>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace feather {
@@ -15,6 +18,32 @@ constexpr int kMaxSplits = 32;
 // The arrival counters occupy a fixed area at the start of every split workspace, whatever the shape, so
 // a workspace reused across shapes never has partial sums where a later call keeps its counters.
 constexpr int64_t kSplitCtrBytes = 64 * 1024;
+
+// Non-temporal weight loads (feather_set_weight_streaming). A weight read once per launch and streamed from HBM
+// loads 4-9% faster with the hint (MI355X, weights of 59-235 MB, working sets past the 256 MB MALL); a working
+// set the MALL could hold (a small model, or one weight timed in a loop) loads up to a third slower, because
+// non-temporal lines are not kept there. In auto mode the hint goes to weights from kStreamWeightMinBytes on:
+// a model with weights that large does not fit the MALL, and below it the measured gains were small or losses.
+constexpr int64_t kStreamWeightMinBytes = int64_t{48} << 20;
+constexpr int kStreamOff = 0;
+constexpr int kStreamOn = 1;
+constexpr int kStreamAuto = 2;
+
+// The process-wide mode; FEATHER_OPS_WEIGHT_STREAMING (0, 1 or 2) sets its first value, auto by default.
+std::atomic<int>& stream_mode() {
+    static std::atomic<int> mode{[] {
+        const char* env = std::getenv("FEATHER_OPS_WEIGHT_STREAMING");
+        if (env && std::strcmp(env, "0") == 0) return kStreamOff;
+        if (env && std::strcmp(env, "1") == 0) return kStreamOn;
+        return kStreamAuto;
+    }()};
+    return mode;
+}
+
+bool stream_weight(int64_t weight_bytes) {
+    const int mode = stream_mode().load(std::memory_order_relaxed);
+    return mode == kStreamOn || (mode == kStreamAuto && weight_bytes >= kStreamWeightMinBytes);
+}
 
 bool aligned(const void* ptr, uintptr_t bytes) {
     return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0;
@@ -159,6 +188,7 @@ Params make_params(const uint16_t* a, const uint8_t* b_prepacked, const float* s
     p.kb_total = static_cast<int32_t>((K + 127) / 128 * 8);
     p.col_scale = has_scale == 2 ? 1 : 0;
     p.splits = 1;
+    p.stream_weight = stream_weight(int64_t{p.kb_total} * N * 16) ? 1 : 0;
     return p;
 }
 
@@ -234,4 +264,11 @@ extern "C" bool feather_scaled_mm_splitk_noalloc(const uint16_t* const a, const 
     }
     const TileQuery t{block_warps_m, block_warps_n, unroll_k, repeat_m, repeat_n, prefetch};
     return launch(p, use_fp8_e5m2, a_bf16, output_bf16, t, stream);
+}
+
+extern "C" int feather_set_weight_streaming(const int mode) {
+    using namespace feather;
+    if (mode == -1) return stream_mode().load();
+    if (mode != kStreamOff && mode != kStreamOn && mode != kStreamAuto) return -1;
+    return stream_mode().exchange(mode);
 }

@@ -72,6 +72,9 @@ struct Params {
     // Ring kernel: workgroups [0, reads_first_blocks) take the reads-first operand schedule, the rest the
     // interleaved one (0: all interleaved). The launcher picks it from the grid's CU occupancy.
     int32_t reads_first_blocks;
+    // The weight may be loaded non-temporally (set by the C ABI from the weight's size and the process-wide
+    // mode): the launcher does so for tiles whose launch reads each weight byte once (M within one tile row).
+    int32_t stream_weight;
 };
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -79,8 +82,14 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
                                              static_cast<int>(bytes), kRsrcFlags);
 }
 
+// Cache-policy operand of a buffer load: 0 (the default), or kCpolNt, the non-temporal hint. A weight read
+// once per launch and streamed from HBM loads faster with it (the caches do not keep its lines); data that a
+// later launch would find in the 256 MB MALL loads slower, since nt lines are not kept there.
+constexpr int kCpolNt = 2;
+
+template <int kCpol = 0>
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off, uint32_t soff = 0) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), static_cast<int>(soff), 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), static_cast<int>(soff), kCpol);
 }
 
 __device__ __forceinline__ u32x2 buf_load8(rsrc_t r, uint32_t off) {
@@ -405,10 +414,11 @@ __device__ __forceinline__ void wait_ring_stage(int r) {
 
 // 16 bytes per lane from buffer offset voff + soff straight into LDS at lds_dst + 16 * lane (lds_dst is
 // wave-uniform). soff is a scalar (SGPR) offset, so a per-lane offset computed once can walk K.
+template <int kCpol = 0>
 __device__ __forceinline__ void dma16(rsrc_t r, const uint8_t* lds_dst, uint32_t voff, uint32_t soff = 0) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)(reinterpret_cast<uintptr_t>(lds_dst)), 16,
-        static_cast<int>(voff), static_cast<int>(soff), 0, 0);
+        static_cast<int>(voff), static_cast<int>(soff), 0, kCpol);
 }
 
 constexpr int gcd(int a, int b) {
@@ -545,7 +555,9 @@ constexpr int lds_epilogue_bytes() {
 // kSplitK: this launch splits K (p.splits > 1). A separate instantiation, so the unsplit kernel carries no
 // join code (its partial reads raise register pressure: measured 3% slower on a 128 x 256 tile).
 // kDeep: the deep-ring variant of a 64-row tile (DmaShape), chosen by the launcher for small grids.
-template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK, bool kDeep>
+// kNtWeight: the weight's direct loads carry the non-temporal hint (launches that read the weight once).
+template <int WM, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK, bool kDeep,
+          bool kNtWeight = false>
 __global__ __launch_bounds__(kWave * WM * WN)
 __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPerEu))) void ring_dma_kernel(
     const Params p) {
@@ -665,12 +677,15 @@ __attribute__((amdgpu_waves_per_eu(DmaShape<WM, WN, U, RM, RN, kDeep>::kWavesPer
         const uint32_t soff = static_cast<uint32_t>(stage) * b_stage_stride;
         if (stage < full_stages) {
 #pragma unroll
-            for (int i = 0; i < S::kBInstr; ++i) dma16(b_rsrc, base + (wave + i * S::kWaves) * 1024, b_off[i], soff);
+            for (int i = 0; i < S::kBInstr; ++i) {
+                dma16<kNtWeight ? kCpolNt : 0>(b_rsrc, base + (wave + i * S::kWaves) * 1024, b_off[i], soff);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < S::kBInstr; ++i) {
                 const bool ok = stage * U + b_chunk[i] < k_chunks;
-                dma16(b_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? b_off[i] : kOob, soff);
+                dma16<kNtWeight ? kCpolNt : 0>(b_rsrc, base + (wave + i * S::kWaves) * 1024, ok ? b_off[i] : kOob,
+                                               soff);
             }
         }
     };
@@ -1011,7 +1026,9 @@ struct StreamShape {
     static_assert(kLoadsPerFetch < 64, "vmcnt range");
 };
 
-template <int KS, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK>
+// kNtWeight: the weight loads carry the non-temporal hint (launches that read the weight once).
+template <int KS, int WN, int U, int RM, int RN, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK,
+          bool kNtWeight = false>
 __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p) {
     using S = StreamShape<KS, WN, U, RM, RN>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
@@ -1113,7 +1130,7 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
                 const uint32_t off = (b_base[j] == kOob || !in_k)
                                          ? kOob
                                          : b_base[j] + static_cast<uint32_t>(chunk) * b_chunk_stride;
-                f.b[q][j] = buf_load16(b_rsrc, off);
+                f.b[q][j] = buf_load16<kNtWeight ? kCpolNt : 0>(b_rsrc, off);
             }
         }
     };

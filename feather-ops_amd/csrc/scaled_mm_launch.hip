@@ -20,6 +20,35 @@ constexpr bool kABf16 = FEATHER_A_BF16 != 0;
 constexpr bool kOutBf16 = FEATHER_OUT_BF16 != 0;
 constexpr int kCus = 256;                // MI355X compute units
 
+// Non-temporal weight loads (Params::stream_weight) go to launches whose M fits one tile row, so that each
+// weight byte is read by one workgroup row. Ring tiles get the variant only at 64 rows or fewer: those are the
+// tiles the heuristic streams big weights with at small M, and the 128-row tiles keep their instantiations.
+template <int WM, int WN, int U, int RM, int RN, bool kSplitK, bool kDeep>
+void launch_ring(const Params& q, dim3 grid, hipStream_t stream) {
+    using S = DmaShape<WM, WN, U, RM, RN>;
+    if constexpr (S::kBM <= 64) {
+        if (q.stream_weight && q.M <= S::kBM) {
+            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, kSplitK, kDeep, true>),
+                               grid, dim3(S::kThreads), 0, stream, q);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, kSplitK, kDeep>), grid,
+                       dim3(S::kThreads), 0, stream, q);
+}
+
+template <int KS, int WN, int U, int RM, int RN, bool kSplitK>
+void launch_stream(const Params& p, dim3 grid, hipStream_t stream) {
+    using S = StreamShape<KS, WN, U, RM, RN>;
+    if (p.stream_weight && p.M <= S::kBM) {
+        hipLaunchKernelGGL((stream_kernel<KS, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, kSplitK, true>), grid,
+                           dim3(S::kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((stream_kernel<KS, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, kSplitK>), grid,
+                           dim3(S::kThreads), 0, stream, p);
+    }
+}
+
 template <int WM, int WN, int U, int RM, int RN, int PF>
 bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
     if (t.warps_m != WM || t.warps_n != WN || t.unroll_k != U || t.repeat_m != RM || t.repeat_n != RN ||
@@ -57,32 +86,26 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
             if ((!kABf16 || p.M <= 64) && blocks <= int64_t{kCus} * D::kBlocksPerCu) {
                 const Params q = with_rounds(D::kBlocksPerCu);
                 if (p.splits > 1) {
-                    hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, true>), grid,
-                                       dim3(S::kThreads), 0, stream, q);
+                    launch_ring<WM, WN, U, RM, RN, true, true>(q, grid, stream);
                 } else {
-                    hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, true>),
-                                       grid, dim3(S::kThreads), 0, stream, q);
+                    launch_ring<WM, WN, U, RM, RN, false, true>(q, grid, stream);
                 }
                 return true;
             }
         }
         const Params q = with_rounds(S::kBlocksPerCu);
         if (p.splits > 1) {
-            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true, false>), grid,
-                               dim3(S::kThreads), 0, stream, q);
+            launch_ring<WM, WN, U, RM, RN, true, false>(q, grid, stream);
         } else {
-            hipLaunchKernelGGL((ring_dma_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false, false>), grid,
-                               dim3(S::kThreads), 0, stream, q);
+            launch_ring<WM, WN, U, RM, RN, false, false>(q, grid, stream);
         }
     } else {
         using S = StreamShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         if (p.splits > 1) {
-            hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, true>),
-                               dim3(static_cast<uint32_t>(tiles * p.splits)), dim3(S::kThreads), 0, stream, p);
+            launch_stream<WM, WN, U, RM, RN, true>(p, dim3(static_cast<uint32_t>(tiles * p.splits)), stream);
         } else {
-            hipLaunchKernelGGL((stream_kernel<WM, WN, U, RM, RN, kE5M2, kABf16, kOutBf16, false>),
-                               dim3(static_cast<uint32_t>(tiles)), dim3(S::kThreads), 0, stream, p);
+            launch_stream<WM, WN, U, RM, RN, false>(p, dim3(static_cast<uint32_t>(tiles)), stream);
         }
     }
     return true;

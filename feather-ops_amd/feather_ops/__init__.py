@@ -18,6 +18,7 @@ from .scaled_mm import (  # noqa: E402
     scaled_mm_hip,
     select_scaled_mm_config,
     select_scaled_mm_splits,
+    set_weight_streaming,
     tile_shape,
 )
 
@@ -31,6 +32,7 @@ __all__ = [
     "scaled_mm_hip",
     "select_scaled_mm_config",
     "select_scaled_mm_splits",
+    "set_weight_streaming",
     "tile_shape",
     "to_scaled_mm_linear",
 ]

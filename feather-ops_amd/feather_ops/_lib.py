@@ -4,6 +4,7 @@ There is no fallback: if the extension is not built, importing `feather_ops` fai
 command, and the ops only have a CUDA (HIP) dispatch key, so CPU tensors are rejected by the dispatcher.
 """
 
+import ctypes
 import pathlib
 
 HERE = pathlib.Path(__file__).resolve().parent
@@ -24,6 +25,22 @@ def load() -> None:
     from . import _C  # noqa: F401  registers the feather_ops torch library
 
     _loaded = True
+
+
+_c_library = None
+
+
+def c_library() -> ctypes.CDLL:
+    """The HIP library's C ABI through ctypes, for the entry points no torch op wraps (the handle is the one
+    `_C` already loaded: the same file)."""
+    global _c_library
+    if _c_library is None:
+        load()
+        lib = ctypes.CDLL(str(LIBRARY))
+        lib.feather_set_weight_streaming.restype = ctypes.c_int
+        lib.feather_set_weight_streaming.argtypes = [ctypes.c_int]
+        _c_library = lib
+    return _c_library
 
 
 def require_native() -> None:

@@ -529,6 +529,29 @@ def clear_split_workspaces() -> None:
     _split_workspaces.clear()
 
 
+_STREAMING_MODES = ("off", "on", "auto")
+
+
+def set_weight_streaming(mode: str | None = None) -> str:
+    """Choose non-temporal weight loads for every later launch in this process and return the previous mode
+    (with `mode=None`, only return the current one). A launch whose M fits one row of its tile reads every
+    weight byte once, and then loads the weight non-temporally:
+
+    - "auto" (the default): when the prepacked weight holds at least 48 MiB;
+    - "on": always;
+    - "off": never.
+
+    A cache hint only; results are the same in every mode. It pays when the weight streams from HBM on every
+    launch (a model far larger than the GPU's 256 MB MALL: 4-9% on weights of 59-235 MB) and costs when the
+    working set would stay in the MALL (up to a third slower): "off" suits small models and one weight timed
+    in a loop. The environment variable FEATHER_OPS_WEIGHT_STREAMING (0, 1 or 2) sets the first value. C ABI:
+    `feather_set_weight_streaming`. No counterpart in the reference."""
+    if mode is not None and mode not in _STREAMING_MODES:
+        raise ValueError(f"weight streaming mode must be one of {_STREAMING_MODES}, got {mode!r}")
+    previous = _lib.c_library().feather_set_weight_streaming(-1 if mode is None else _STREAMING_MODES.index(mode))
+    return _STREAMING_MODES[previous]
+
+
 def _launch(
     a: torch.Tensor,
     b_prepacked: torch.Tensor,

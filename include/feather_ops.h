@@ -107,6 +107,22 @@ int64_t feather_splitk_workspace_bytes(int64_t M, int64_t N, int64_t K, int bloc
                                        int unroll_k, int repeat_m, int repeat_n, bool prefetch, int splits);
 
 /*
+ * Process-wide choice of non-temporal weight loads, for the three scaled_mm entry points above; returns the
+ * previous mode, the current one for mode = -1, or -1 (nothing changed) for any other value. Results do not
+ * depend on it: it is a cache hint. A launch whose M fits one row of its tile (so that it reads every weight
+ * byte once) then loads the weight non-temporally:
+ *   0  never;
+ *   1  always;
+ *   2  (auto, the default) when the prepacked weight holds at least 48 MiB.
+ * The hint pays when the weight streams from HBM on every launch (a model far larger than the GPU's 256 MB
+ * MALL: 4-9% on weights of 59-235 MB) and costs when the caller's working set would stay in the MALL (up to
+ * a third slower): mode 0 suits small models and one weight timed in a loop. The environment variable
+ * FEATHER_OPS_WEIGHT_STREAMING (0, 1 or 2) sets the first value. No counterpart in the reference, whose
+ * GPUs have no such cache.
+ */
+int feather_set_weight_streaming(int mode);
+
+/*
  * out[i] = bf16 -> fp16 of in[i] with round-toward-zero (finite overflow saturates to +-65504, inf/NaN
  * pass through), n elements, enqueued on `stream`. Replaces the reference's Triton kernel behind
  * feather_ops/convert.py:24-34 (bf16_to_fp16), which has no C entry point of its own. in/out 16-byte

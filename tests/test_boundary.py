@@ -18,7 +18,7 @@ HEADER = ROOT / "include" / "feather_ops.h"
 
 def _declared():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return re.findall(r"^\s*(?:bool|int64_t)\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:bool|int64_t|int)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 @pytest.fixture(scope="module")
@@ -42,6 +42,8 @@ def lib():
     handle.feather_scaled_mm_splitk_noalloc.restype = ctypes.c_bool
     handle.feather_scaled_mm_splitk_noalloc.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + \
         [ctypes.c_int] * 2 + [ctypes.c_bool] * 3 + [ctypes.c_int] * 5 + [ctypes.c_bool, ctypes.c_int, ctypes.c_void_p]
+    handle.feather_set_weight_streaming.restype = ctypes.c_int
+    handle.feather_set_weight_streaming.argtypes = [ctypes.c_int]
     handle.feather_splitk_workspace_bytes.restype = ctypes.c_int64
     handle.feather_splitk_workspace_bytes.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int] * 5 + \
         [ctypes.c_bool, ctypes.c_int]
@@ -52,9 +54,49 @@ def test_library_exports_every_declared_symbol(lib):
     names = _declared()
     assert set(names) == {"launch_scaled_mm", "feather_bf16_to_fp16", "feather_widen_bf16", "feather_prepack_b",
                           "feather_scaled_mm_splitk", "feather_splitk_workspace_bytes",
-                          "feather_scaled_mm_splitk_noalloc"}
+                          "feather_scaled_mm_splitk_noalloc", "feather_set_weight_streaming"}
     for name in names:
         assert hasattr(lib, name), name
+
+
+def test_weight_streaming_mode_round_trips(lib):
+    """The C ABI's process-wide mode: -1 queries, 0/1/2 set and return the previous mode, anything else is
+    refused (-1) and changes nothing; the Python wrapper maps the same modes to names."""
+    import feather_ops
+
+    first = lib.feather_set_weight_streaming(-1)
+    assert first in (0, 1, 2)
+    try:
+        assert lib.feather_set_weight_streaming(0) == first
+        assert lib.feather_set_weight_streaming(1) == 0
+        assert lib.feather_set_weight_streaming(-1) == 1
+        for bad in (3, -2, 99):
+            assert lib.feather_set_weight_streaming(bad) == -1
+            assert lib.feather_set_weight_streaming(-1) == 1
+        assert lib.feather_set_weight_streaming(2) == 1
+        assert feather_ops.set_weight_streaming() == "auto"
+        assert feather_ops.set_weight_streaming("off") == "auto"
+        assert lib.feather_set_weight_streaming(-1) == 0
+        with pytest.raises(ValueError):
+            feather_ops.set_weight_streaming("sometimes")
+        assert feather_ops.set_weight_streaming("on") == "off"
+    finally:
+        lib.feather_set_weight_streaming(first)
+
+
+@pytest.mark.parametrize("env,want", [(None, "auto"), ("0", "off"), ("1", "on"), ("2", "auto"), ("yes", "auto")])
+def test_weight_streaming_mode_starts_from_the_environment(env, want):
+    import os
+    import subprocess
+    import sys
+
+    environ = {k: v for k, v in os.environ.items() if k != "FEATHER_OPS_WEIGHT_STREAMING"}
+    if env is not None:
+        environ["FEATHER_OPS_WEIGHT_STREAMING"] = env
+    code = "import feather_ops; print(feather_ops.set_weight_streaming())"
+    got = subprocess.run([sys.executable, "-c", code], env=environ, cwd=ROOT / "feather-ops_amd", check=True,
+                         capture_output=True, text=True, timeout=300).stdout.split()[-1]
+    assert got == want
 
 
 # Fake, 16-byte aligned device addresses: every call below is refused before anything dereferences them.

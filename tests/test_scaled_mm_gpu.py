@@ -476,6 +476,39 @@ def test_decode_is_exact_on_every_finite_code(fo, fp8, tile):
     assert torch.equal(out.cpu().view(torch.int16)[nonzero], want.view(torch.int16)[nonzero])
 
 
+@pytest.mark.parametrize("tile,m,n,k,splits", [
+    ((4, 1, 4, 1, 4, 0), 16, 2048, 2048, 1),     # streaming tile, one tile row
+    ((8, 1, 4, 1, 2, 0), 2, 1024, 8192, 2),      # streaming tile split across workgroups
+    ((2, 2, 4, 2, 2, 0), 32, 1024, 1040, 1),     # 32-row streaming tile
+    ((2, 2, 4, 2, 2, 1), 48, 3000, 1040, 1),     # 64-row ring tile, deep ring
+    ((1, 4, 4, 4, 2, 1), 64, 3000, 2048, 4),     # 64 x 128 ring tile, deep ring, split 4 ways
+    ((2, 2, 4, 2, 2, 1), 40, 70400, 1040, 1),    # 1100 tiles: the shallow ring
+    ((2, 2, 4, 4, 4, 1), 100, 2048, 1040, 1),    # 128-row tile: no non-temporal variant
+    ((4, 1, 4, 1, 4, 0), 40, 2048, 1040, 1),     # three tile rows: the default loads
+])
+@pytest.mark.parametrize("a_dtype", [torch.float16, torch.bfloat16])
+def test_weight_streaming_modes_are_bit_identical(fo, tile, m, n, k, splits, a_dtype):
+    """Non-temporal weight loads are a cache hint: every mode returns the same bits, on every kernel that has
+    the variant (streaming and 64-row ring tiles, split or not, deep or shallow ring) and on launches that
+    keep the default loads; the "on" output also against the oracle."""
+    a = _tensor((m, k), a_dtype)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=1))
+    s = torch.tensor(0.25, device="cuda")
+    bias = _tensor((n,), a_dtype, seed=2)
+    previous = fo.set_weight_streaming("on")
+    try:
+        on = fo.scaled_mm_hip(a, bp, s, bias, a_dtype, tile=tile, splits=splits)
+        fo.set_weight_streaming("off")
+        off = fo.scaled_mm_hip(a, bp, s, bias, a_dtype, tile=tile, splits=splits)
+        fo.set_weight_streaming("auto")
+        auto = fo.scaled_mm_hip(a, bp, s, bias, a_dtype, tile=tile, splits=splits)
+    finally:
+        fo.set_weight_streaming(previous)
+    assert torch.equal(on.view(torch.int16), off.view(torch.int16))
+    assert torch.equal(auto.view(torch.int16), off.view(torch.int16))
+    check_against_oracle(on, a, bp, s, bias, rows=None if m * n <= (1 << 20) else sample_rows(m, n_random=16))
+
+
 def test_deterministic(fo):
     a = _tensor((300, 512), torch.float16)
     bp = fo.prepack_b_for_scaled_mm(_tensor((512, 1000), torch.float8_e5m2, seed=1))

@@ -105,8 +105,9 @@ def _check_lds():
 def test_every_kernel_allocates_exactly_its_tiles_lds():
     """The LDS audit (check_lds.py, the reference's tools/check_lds.py role): the compiled gfx950 code
     object's group_segment_fixed_size of every ring (unsplit and split, shallow and, for 64-row tiles, deep)
-    and streaming instantiation (unsplit and split) equals the size the tile asks for. Compiles one dtype
-    combination (hipcc, device code only)."""
+    and streaming instantiation (unsplit and split), and of the non-temporal-weight variants of the streaming
+    and 64-row ring ones, equals the size the tile asks for. Compiles one dtype combination (hipcc, device
+    code only)."""
     from feather_ops.tiles import SCALED_MM_TILES
 
     check = _check_lds()
@@ -115,8 +116,10 @@ def test_every_kernel_allocates_exactly_its_tiles_lds():
     asm = check.compile_asm("100")
     checked, bad = check.audit(asm)
     small_ring = sum(1 for t in SCALED_MM_TILES if t[5] == 1 and 16 * t[0] * t[3] <= 64)
+    streaming = sum(1 for t in SCALED_MM_TILES if t[5] == 0)
     assert small_ring == 2
-    assert checked == 2 * len(SCALED_MM_TILES) + 2 * small_ring
+    non_temporal = 2 * streaming + 4 * small_ring
+    assert checked == 2 * len(SCALED_MM_TILES) + 2 * small_ring + non_temporal
     assert bad == []
     # a planted off-by-one in the expectation is caught for every instantiation
     real = check.expected_bytes
