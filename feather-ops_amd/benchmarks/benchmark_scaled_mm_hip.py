@@ -47,6 +47,7 @@ from feather_ops.scaled_mm import (  # noqa: E402
     prepack_b_for_scaled_mm,
     select_scaled_mm_config,
     select_scaled_mm_splits,
+    set_weight_streaming,
 )
 from feather_ops.tiles import SCALED_MM_TILES, gemm_block_sizes, split_workspace_bytes  # noqa: E402
 
@@ -76,8 +77,11 @@ def parse_tiles(text: str) -> list[tuple[int, ...]]:
     return tiles
 
 
-def weight_copies(n: int, k: int, cold: bool) -> int:
-    """Copies of the prepacked weight to rotate over: enough to exceed the 256 MB MALL twice when cold."""
+def weight_copies(n: int, k: int, cold: bool, copies: int | None = None) -> int:
+    """Copies of the prepacked weight to rotate over: `copies` if given, else enough to exceed the 256 MB MALL
+    twice when cold and one otherwise."""
+    if copies is not None:
+        return copies
     if not cold:
         return 1
     k_pad = -(-k // 128) * 128
@@ -93,7 +97,7 @@ def run_cell(m: int, n: int, k: int, tiles, args) -> dict:
     b_kn = torch.randn((k, n), generator=gen, device="cuda").to(fp8)
     scale = torch.tensor(2.34, device="cuda", dtype=torch.float32)
     bias = torch.randn(n, generator=gen, device="cuda").to(out_dtype) if args.bias else None
-    copies = weight_copies(n, k, args.cold)
+    copies = weight_copies(n, k, args.cold, args.copies)
     packed = prepack_b_for_scaled_mm(b_kn)
     packs = [packed] + [packed.clone() for _ in range(copies - 1)]
     control_w = (b_kn.t().float() * scale).to(torch.bfloat16).contiguous()
@@ -187,6 +191,10 @@ def main() -> int:
     parser.add_argument("--fp8", choices=list(_FP8), default="e5m2", help="weight format")
     parser.add_argument("--no-bias", dest="bias", action="store_false")
     parser.add_argument("--cold", action="store_true", help="rotate weight copies past the 256 MB MALL")
+    parser.add_argument("--copies", type=int, default=None,
+                        help="rotate exactly this many weight copies (a working set of that many weights)")
+    parser.add_argument("--weight-streaming", choices=["auto", "on", "off"], default=None,
+                        help="non-temporal weight loads (feather_ops.set_weight_streaming); default: leave the mode")
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--rounds", type=int, default=5)
     parser.add_argument("--target-ms", type=float, default=20.0)
@@ -200,6 +208,10 @@ def main() -> int:
         print("needs a GPU", file=sys.stderr)
         return 2
 
+    if args.copies is not None and args.copies < 1:
+        parser.error("--copies must be at least 1")
+    if args.weight_streaming is not None:
+        set_weight_streaming(args.weight_streaming)
     tiles = parse_tiles(args.tiles) if args.tiles is not None else []
     args.splits = [int(v) for v in args.splits.split(",") if v.strip()]
     if args.square:
