@@ -501,7 +501,7 @@ def main() -> int:
     sk = time_split_cell(512, 5120, 5376, (2, 2, 4, 2, 2, 1), rounds) if sec else None
     # a decoder's down projection at batch 2: 64 tiles of 16 x 64, 67 MB of weight, 8 rotated copies; the
     # unsplit control is the streaming tile the heuristic picks without split-K (16 x 16, 256 blocks)
-    dk = time_split_cell(2, 16384, 4096, (8, 1, 4, 1, 1, 0), rounds, copies=8) if sec else None
+    dk = time_split_cell(2, 16384, 2048, (8, 1, 4, 1, 1, 0), rounds, copies=16) if sec else None
     cpu = None if args.no_cpu else time_cpu_baseline()
 
     t3 = c3["t"]
@@ -570,8 +570,8 @@ def main() -> int:
                                "tile": sk["tile"], "splits": sk["splits"], **sk["auto"],
                                "unsplit_tile": sk["unsplit_tile"], "unsplit": sk["unsplit"]}
     if dk is not None:
-        line["decode_split_cell"] = {"workload": "skinny long K: fp16 [2,16384] x e5m2 [4096,16384] -> fp16, "
-                                                 "8 rotated weights",
+        line["decode_split_cell"] = {"workload": "skinny long K: fp16 [2,16384] x e5m2 [2048,16384] -> fp16, "
+                                                 "16 rotated weights",
                                      "tile": dk["tile"], "splits": dk["splits"], **dk["auto"],
                                      "frac_hbm_peak": round(dk["auto"]["GBps"] / PEAK_HBM_GBPS, 4),
                                      "unsplit_tile": dk["unsplit_tile"], "unsplit": dk["unsplit"]}

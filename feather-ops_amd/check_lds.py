@@ -43,7 +43,9 @@ def expected_bytes(kernel: str, ints: list[int], bools: list[int] = ()) -> int:
         b_stage = 16 * warps_n * repeat_n * unroll_k * 16
         return slots_a * a_stage + slots_b * b_stage
     k_slices, warps_n, unroll_k, repeat_m, repeat_n = ints
-    activations = k_slices * warps_n * 2 * (unroll_k // 4) * repeat_m * 2048
+    # fetches in flight per wave (StreamShape::kDepth)
+    depth = 3 if k_slices * warps_n * repeat_n * (unroll_k // 4) <= 8 and repeat_m <= 2 else 2
+    activations = k_slices * warps_n * depth * (unroll_k // 4) * repeat_m * 2048
     join = (k_slices if k_slices > 1 else 0) * warps_n * repeat_m * repeat_n * 64 * 16
     return activations + join
 

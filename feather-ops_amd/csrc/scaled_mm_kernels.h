@@ -1013,17 +1013,24 @@ struct StreamShape {
     static constexpr int kGroups = U / 4;             // 64-deep groups per iteration of one wave
     static constexpr int kFrags = WN * RM * RN;       // 16 x 16 output fragments of the block
     static constexpr int kRedBytes = (KS > 1 ? KS : 0) * kFrags * kWave * 16;
-    // Activations: per wave, a double buffer of one iteration's fragments (16 rows x 64 k x 2 bytes each).
+    // Fetches a wave keeps in flight. One fetch of the whole block carries KS * WN * RN * kGroups KiB of weight
+    // (1 KiB per wave, 16-column fragment and 64-deep group); blocks whose fetch carries at most 8 KiB go
+    // three deep, so that 12-24 KiB of weight stay in flight per block, and wider ones two (16-64 KiB), where a
+    // third fetch measured slower. Blocks of 4 fragment rows (RM = 4) move 4x the activations per fetch and
+    // keep two.
+    static constexpr int kDepth = (KS * WN * RN * kGroups <= 8 && RM <= 2) ? 3 : 2;
+    // Activations: per wave, one buffer per fetch in flight of one iteration's fragments (16 rows x 64 k x
+    // 2 bytes each).
     static constexpr int kAFragBytes = 2048;
     static constexpr int kABufBytes = kGroups * RM * kAFragBytes;
-    static constexpr int kAWaveBytes = 2 * kABufBytes;
+    static constexpr int kAWaveBytes = kDepth * kABufBytes;
     static constexpr int kALdsBytes = KS * WN * kAWaveBytes;
     static constexpr int kLdsBytes = kALdsBytes + kRedBytes;
     static constexpr int kLoadsPerFetch = kGroups * (2 * RM + RN);  // vector-memory ops of one fetch
     static_assert(U % 4 == 0, "an iteration is a whole number of 64-deep MFMA groups");
     static_assert(kThreads <= 1024, "block size");
     static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
-    static_assert(kLoadsPerFetch < 64, "vmcnt range");
+    static_assert((kDepth - 1) * kLoadsPerFetch < 64, "vmcnt range");
 };
 
 // kNtWeight: the weight loads carry the non-temporal hint (launches that read the weight once).
@@ -1168,34 +1175,45 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
         }
     };
 
-    // Iterations of this wave: groups ks, ks + KS, ... taken kGroups at a time; fetch it + 1 is in flight
-    // while iteration it computes. Before a consume, this wave's loads of that iteration have landed
-    // (vector-memory operations retire in issue order, so only the newer fetch may stay outstanding). The
-    // loop body is straight-line: its second fetch goes out even in the last pair of iterations, where it
-    // loads zeros that are never consumed.
+    // Iterations of this wave: groups ks, ks + KS, ... taken kGroups at a time; fetches it + 1 .. it + kDepth - 1
+    // are in flight while iteration it computes, in buffers (it + d) % kDepth. Before a consume, this wave's
+    // loads of that iteration have landed (vector-memory operations retire in issue order, so only the
+    // kDepth - 1 newer fetches may stay outstanding). The loop body is straight-line: its fetches go out even
+    // in the last round of iterations, where they load zeros that are never consumed.
     // Scheduling barriers keep each fetch ahead of the decode of the iteration before it (left alone, the
     // compiler hoists that decode above the fetch, and its register wait then retires the older fetch before
     // the newer one is issued).
+    constexpr int D = S::kDepth;
     const int per_iter = S::kGroups * KS;
     const int iters = (group_end - group0 + per_iter - 1) / per_iter;
-    Frag f0, f1;
-    fetch(f0, 0, 0);
-    int it = 0;
-    for (; it + 1 < iters; it += 2) {
+    Frag f[D];
+#pragma unroll
+    for (int d = 0; d + 1 < D; ++d) {
         __builtin_amdgcn_sched_barrier(0);
-        fetch(f1, 1, it + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
-        consume(f0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        fetch(f0, 0, it + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerFetch));
-        consume(f1, 1);
+        fetch(f[d], d, d);
     }
-    if (it < iters) {  // an odd count: the last fetch is a real one
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        consume(f0, 0);
+    int it = 0;
+    for (; it + D - 1 < iters; it += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(f[(d + D - 1) % D], (d + D - 1) % D, it + d + D - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 1) * S::kLoadsPerFetch));
+            consume(f[d], d);
+        }
+    }
+    // The last iterations (fewer than D): fetches it .. it + D - 2 are in flight, in buffers 0 .. D - 2.
+    static_assert(D == 2 || D == 3, "the tail below is written out for these depths");
+    if (it < iters) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 2) * S::kLoadsPerFetch));
+        consume(f[0], 0);
+    }
+    if constexpr (D == 3) {
+        if (it + 1 < iters) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            consume(f[1], 1);
+        }
     }
 
     if constexpr (KS > 1) {

@@ -133,6 +133,12 @@ _STREAM_SPLIT_COUNTS = (8, 6, 4, 3, 2)
 _STREAM_SPLIT_MIN_RANGE = 3072
 _STREAM_SPLIT_MIN_WORKGROUPS = 128
 _STREAM_SPLIT_CAP_PER_ROW = 64
+# Except: M <= _STREAM_UNSPLIT_TINY_M on a weight whose 16-column fragments fill one round of 192-256 blocks
+# (N 3072-4096) and K up to _STREAM_UNSPLIT_MAX_K runs unsplit on the 16 x 16 tile, which keeps three fetches
+# in flight per wave: 1.02-1.2x over the 16 x 32 tile split 2 ways on 21 of 24 cells (M 1-4, K 8192-16384;
+# same-box A/B, cold weights), while at K 18944-28672 splitting stays ahead or even.
+_STREAM_UNSPLIT_TINY_M = 4
+_STREAM_UNSPLIT_MAX_K = 16384
 
 # bf16 activations: the auto path widens them once up front (feather_ops::widen_bf16, the kernels' own
 # round-to-nearest-even conversion, so the result is the same bits) and runs the fp16-activation kernel when
@@ -175,6 +181,8 @@ def _stream_split(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int
     """(tile, splits) for the long-K streaming regime, or None where the unsplit streaming rule applies (see
     _STREAM_SPLIT_MIN_K above). Measured with the tile sweep on 48 decoder-shaped cells (M 1-32, N 2048-28672,
     K 3072-28672) and the grid's skinny cells, fp16 and bf16, graph-timed with cold weights."""
+    if M <= _STREAM_UNSPLIT_TINY_M and 3 * _CUS // 4 <= N // 16 <= _CUS and K <= _STREAM_UNSPLIT_MAX_K:
+        return None
     tiny = M <= _STREAM_TINY_M
     tile = _TILE_STREAM_16x32 if tiny else _TILE_STREAM_16x64_KS4
     tiles = _blocks(M, N, tile)

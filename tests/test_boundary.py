@@ -337,8 +337,14 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(16, 14336, 4096)[1] == 1
     # skinny M, long K, fewer than 171 16 x 64 tiles: a streaming tile split to at most one workgroup per CU
     # (the 16 x 32 tile for M <= 12, the 16 x 64 tile with 4 K slices above), each K range 3072 deep or more
-    assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 2, 0), 2)      # 128 tiles of 16 x 32 -> 256 workgroups
-    assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 2, 0), 2)
+    assert auto(2, 2048, 16384) == ((8, 1, 4, 1, 2, 0), 4)      # 64 tiles of 16 x 32 -> 256 workgroups
+    assert auto(6, 4096, 14336) == ((8, 1, 4, 1, 2, 0), 2)      # 128 tiles of 16 x 32 -> 256 workgroups
+    assert auto(1, 4096, 28672) == ((8, 1, 4, 1, 2, 0), 2)
+    # except M <= 4 with 192-256 blocks of 16 x 16 and K <= 16384: that tile unsplit (three fetches in flight)
+    assert auto(2, 4096, 16384) == ((8, 1, 4, 1, 1, 0), 1)
+    assert auto(1, 4096, 14336) == ((8, 1, 4, 1, 1, 0), 1)
+    assert auto(4, 3072, 12288) == ((8, 1, 4, 1, 1, 0), 1)
+    assert auto(4, 3584, 18944) == ((8, 1, 4, 1, 2, 0), 2)
     assert auto(1, 8192, 28672) == ((8, 1, 4, 1, 2, 0), 1)      # 256 tiles of 16 x 32: no split needed
     assert auto(16, 4096, 16384) == ((4, 1, 4, 1, 4, 0), 4)     # 64 tiles of 16 x 64 -> 256 workgroups
     assert auto(16, 5120, 13824) == ((4, 1, 4, 1, 4, 0), 3)     # 80 tiles -> 240

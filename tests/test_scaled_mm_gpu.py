@@ -196,7 +196,8 @@ def test_ring_operand_schedules(fo, tile, n_tiles, splits, a_dtype):
 # wave-quantization choice among 128 x 128 / 128 x 256): the auto path on the tile it picks, bf16 in and out
 # with a bias, against the oracle.
 HEURISTIC_CELLS = [
-    (2, 4096, 16384),    # 16 x 32 streaming tile split 2 ways along K across workgroups
+    (2, 2048, 16384),    # 16 x 32 streaming tile split 4 ways along K across workgroups
+    (2, 4096, 16384),    # 16 x 16 streaming tile unsplit, three fetches in flight per wave
     (16, 5120, 13824),   # 16 x 64 streaming tile, 4 slices, split 3 ways
     (1, 17408, 4096),    # 16 x 32 columns: 64-column blocks would leave a small second round
     (16, 4096, 4096),    # 16 x 16 columns, 8 slices
