@@ -306,7 +306,9 @@ def select_scaled_mm_config(
     - M <= 16 with 512 to 1024 64 x 128 tiles (N from 65536 to 131072, LM-head widths): that ring tile,
       whose direct-to-LDS weight stream runs 5-12% faster than the streaming tiles there; beyond 1024
       tiles the second, partial wave of blocks makes it slower.
-    - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks.
+    - 16 < M <= 32: the 32-row streaming tile when it gives more than 384 blocks, or 192-256 (one round:
+      1.03-1.28x over two rows of the 16 x 64 tile on 24 cells, M 20-32, N 12288-16384, K 4096-5120, with
+      three fetches in flight; at 288 blocks the small second round loses 6%).
     - K >= 8192 with at most 170 16 x 64 streaming tiles: the 16 x 32 tile (8 K slices) for M <= 12, the
       16 x 64 tile (4 K slices) above, split along K to at most one workgroup per CU
       (`select_scaled_mm_splits`), where that gives more workgroups than the unsplit rule below.
@@ -336,7 +338,8 @@ def select_scaled_mm_config(
         ring_tiles = _blocks(M, N, _TILE_RING_64x128)
         if ring_tiles >= 2 * _CUS and (M > 16 or ring_tiles <= 4 * _CUS):
             return _TILE_RING_64x128
-    if 16 < M <= 32 and _blocks(M, N, _TILE_STREAM_32x64) > 3 * _CUS // 2:
+    blocks_32 = _blocks(M, N, _TILE_STREAM_32x64)
+    if 16 < M <= 32 and (blocks_32 > 3 * _CUS // 2 or 3 * _CUS // 4 <= blocks_32 <= _CUS):
         return _TILE_STREAM_32x64
     if K >= _STREAM_SPLIT_MIN_K and _blocks(M, N, _TILE_STREAM_16x64) < _STREAM_SPLIT_MAX_TILES:
         split = _stream_split(M, N, K)

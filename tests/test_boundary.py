@@ -375,7 +375,8 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(32, 65536, 4096) == ((1, 4, 4, 4, 2, 1), 1)     # M <= 32: from a 96 MB weight
     assert auto(32, 32768, 4096) == ((1, 4, 4, 4, 2, 1), 2)     # 256 tiles of 64 x 128
     assert auto(32, 5120, 25600) == ((2, 2, 4, 2, 2, 1), 6)     # 80 tiles, long K
-    assert auto(32, 16384, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 256 32-row tiles: the 16-row tile
+    assert auto(32, 16384, 4096) == ((2, 2, 4, 2, 2, 0), 1)     # 256 32-row tiles: one round of them
+    assert auto(24, 18432, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 288: a small second round, the 16-row tile
     assert auto(40, 8448, 10496) == ((2, 2, 4, 2, 2, 1), 3)     # 132 tiles: 4 splits would leave 16 over
     # a pinned tile the heuristic would not pick is never split by it
     assert splits(512, 5376, 5120, (2, 2, 4, 2, 2, 1)) == 1

@@ -203,6 +203,7 @@ HEURISTIC_CELLS = [
     (16, 4096, 4096),    # 16 x 16 columns, 8 slices
     (16, 6144, 6144),    # 16 x 32 columns
     (32, 25600, 2048),   # 32-row streaming tile
+    (20, 14336, 4096),   # 32-row streaming tile, one round of 224 blocks
     (32, 5120, 25600),   # 64 x 64 ring tile at 32 rows, split 6 ways along K (deep ring)
     (64, 16384, 4096),   # 64 x 64 ring tile at 64 rows (deep ring), split 2 ways along K
     (52, 17408, 11264),  # 64 x 128 ring tile at 52 rows (more 64 x 64 tiles than CUs), split 3 ways
