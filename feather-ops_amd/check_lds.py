@@ -3,7 +3,7 @@
 
 The number the runtime allocates is the code object's `group_segment_fixed_size`; the kernels ask for a
 compile-time function of the tile (the ring kernel: its activation and weight rings, `tiles.ring_slots`,
-shallow or deep;
+shallow or deep; the wide kernel: its 3 + 3 slots of 256 x 64 stages;
 the streaming kernel: per-wave activation double buffers plus the K-slice join). A mismatch costs
 occupancy, so it is a bug in the source or the compiler. Same role as the reference's
 `tools/check_lds.py:30-101`, for gfx950: it compiles `csrc/scaled_mm_launch.hip` for one dtype
@@ -35,6 +35,9 @@ def _tiles():
 def expected_bytes(kernel: str, ints: list[int], bools: list[int] = ()) -> int:
     """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`); a ring kernel's fifth template
     flag is its deep-ring variant (the flags after it, such as non-temporal weight loads, leave LDS alone)."""
+    if kernel == "wide_kernel":
+        slots_a, slots_b = _tiles().ring_slots(_tiles().WIDE_TILE)
+        return slots_a * 256 * 64 * 2 + slots_b * 256 * 64
     if kernel == "ring_dma_kernel":
         warps_m, warps_n, unroll_k, repeat_m, repeat_n = ints
         deep = bool(bools[4]) if len(bools) >= 5 else False
@@ -70,7 +73,7 @@ def audit(asm: str) -> tuple[int, list[tuple]]:
     """(instantiations checked, [(kernel, ints, bools, allocated, expected)] that disagree)."""
     # A kernel's mangled name carries its template arguments as `L<type><value>E` tokens after `I`: `i` for
     # the int tile parameters, `b` for the bool flags.
-    kernel_re = re.compile(r"(ring_dma_kernel|stream_kernel)I(.*)")
+    kernel_re = re.compile(r"(ring_dma_kernel|stream_kernel|wide_kernel)I(.*)")
     name, checked, bad = None, 0, []
     for line in asm.splitlines():
         kd = re.match(r"\s*\.amdhsa_kernel\s+(\S+)", line)

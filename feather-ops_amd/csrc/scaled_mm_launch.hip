@@ -7,6 +7,7 @@
 
 #include "feather_tiles.h"
 #include "scaled_mm_kernels.h"
+#include "scaled_mm_wide.h"
 
 #if !defined(FEATHER_B_E5M2) || !defined(FEATHER_A_BF16) || !defined(FEATHER_OUT_BF16)
 #error "compile with -DFEATHER_B_E5M2=<0|1> -DFEATHER_A_BF16=<0|1> -DFEATHER_OUT_BF16=<0|1>"
@@ -55,7 +56,26 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         t.prefetch != (PF != 0)) {
         return false;
     }
-    if constexpr (PF != 0) {
+    if constexpr (PF != 0 && is_wide_tile<WM, WN, U, RM, RN>()) {
+        // One workgroup per CU, one wave per SIMD: the software-pipelined wide kernel.
+        using S = WideShape;
+        const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
+        const dim3 grid(static_cast<uint32_t>(tiles * p.splits));
+        // M, N or K off the tile grid: the instantiation that masks every load per lane.
+        const bool ragged = p.M % S::kBM != 0 || p.N % S::kBN != 0 || p.K % 64 != 0;
+        const auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(S::kThreads), 0, stream, p); };
+        if (p.splits > 1) {
+            if (ragged) {
+                go(wide_kernel<kE5M2, kABf16, kOutBf16, true, true>);
+            } else {
+                go(wide_kernel<kE5M2, kABf16, kOutBf16, true, false>);
+            }
+        } else if (ragged) {
+            go(wide_kernel<kE5M2, kABf16, kOutBf16, false, true>);
+        } else {
+            go(wide_kernel<kE5M2, kABf16, kOutBf16, false, false>);
+        }
+    } else if constexpr (PF != 0) {
         using S = DmaShape<WM, WN, U, RM, RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         const int64_t blocks = tiles * p.splits;

@@ -104,8 +104,8 @@ def _check_lds():
 
 def test_every_kernel_allocates_exactly_its_tiles_lds():
     """The LDS audit (check_lds.py, the reference's tools/check_lds.py role): the compiled gfx950 code
-    object's group_segment_fixed_size of every ring (unsplit and split, shallow and, for 64-row tiles, deep)
-    and streaming instantiation (unsplit and split), and of the non-temporal-weight variants of the streaming
+    object's group_segment_fixed_size of every ring (unsplit and split, shallow and, for 64-row tiles, deep),
+    wide (unsplit and split, whole and ragged shapes) and streaming instantiation (unsplit and split), and of the non-temporal-weight variants of the streaming
     and 64-row ring ones, equals the size the tile asks for. Compiles one dtype combination (hipcc, device
     code only)."""
     from feather_ops.tiles import SCALED_MM_TILES
@@ -119,7 +119,10 @@ def test_every_kernel_allocates_exactly_its_tiles_lds():
     streaming = sum(1 for t in SCALED_MM_TILES if t[5] == 0)
     assert small_ring == 2
     non_temporal = 2 * streaming + 4 * small_ring
-    assert checked == 2 * len(SCALED_MM_TILES) + 2 * small_ring + non_temporal
+    wide = sum(1 for t in SCALED_MM_TILES if t[:6] == (2, 2, 4, 8, 8, 1))
+    assert wide == 1
+    # the wide tile has 4 instantiations (unsplit / split x whole / ragged shapes) where a ring tile has 2
+    assert checked == 2 * len(SCALED_MM_TILES) + 2 * small_ring + non_temporal + 2 * wide
     assert bad == []
     # a planted off-by-one in the expectation is caught for every instantiation
     real = check.expected_bytes
