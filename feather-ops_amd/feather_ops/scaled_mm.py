@@ -33,6 +33,8 @@ _TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
 # tile) it measured even.
 _TILE_RING_128x256_W64 = (1, 4, 4, 8, 4, 1)
 _TILE_RING_256x256 = (4, 2, 4, 4, 8, 1)
+# The wide kernel's tile: 256 x 256 on one workgroup per CU, 4 waves of 128 x 128 (tiles.py `is_wide`).
+_TILE_WIDE = (2, 2, 4, 8, 8, 1)
 _TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
 _TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
 _TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
@@ -64,6 +66,31 @@ _RING_MODEL_FP16 = (
     (_TILE_RING_128x128, 3, 960.0),
     (_TILE_RING_64x128, 3, 600.0),
 )
+
+# The wide tile (fp16 activations; bf16 ones are widened first, `widen_first`): on shapes on its grid (M and N
+# multiples of 256, K of 64: its unmasked load path) with K >= 3072, when its last round of tiles is whole or
+# at least 170 / 256 full, or the grid runs at least 1700 tiles (6.6 rounds); with a single, partial round
+# (fewer than 256 tiles) only from K = 4096. Measured with the tile sweep on the 76 large-grid cells of the
+# grid: on the 21 cells this takes, 1.032x the previous pick in geometric mean (C3 1.040, 4096^2 x 4096 1.067,
+# 5376^2 x 7168 1.044, 9216 x 1280 x 5120 1.073; worst 0.988 at 4096 x 3072 x 3072 before the K rule); it
+# loses on the cells it leaves out: ragged shapes (masked loads, a mostly empty last tile row: 4112 x 4096 x
+# 4096 0.88), partial last rounds of few rounds (288 tiles: 0.75-0.87; 560 and 608: 0.97-0.98, where the ring
+# tiles' two workgroups per CU split the last round more finely) and K <= 2048 (0.87-0.98).
+_WIDE_MIN_K = 3072
+_WIDE_SINGLE_ROUND_MIN_K = 4096
+_WIDE_MIN_LAST_ROUND = 170
+_WIDE_MANY_TILES = 1700
+
+
+def _wide_fits(M: int, N: int, K: int) -> bool:
+    """Whether the fp16-activation heuristic takes the wide tile (see _WIDE_MIN_K)."""
+    if M % 256 or N % 256 or K % 64 or K < _WIDE_MIN_K:
+        return False
+    tiles = (M // 256) * (N // 256)
+    if tiles < _CUS and K < _WIDE_SINGLE_ROUND_MIN_K:
+        return False
+    return tiles % _CUS == 0 or tiles % _CUS >= _WIDE_MIN_LAST_ROUND or tiles >= _WIDE_MANY_TILES
+
 
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
 _SPLIT_MIN_K = 4096
@@ -278,7 +305,10 @@ def select_scaled_mm_config(
     Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile and split count;
     with `select_scaled_mm_splits` the pick is within 0.7% of the best candidate in geometric mean) and
     extra cells where the grid had few:
-    - M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
+    - M > 64 and at least one CU's worth of 128 x 128 tiles, fp16 activations, on the wide tile's grid (M and N
+      multiples of 256, K of 64) with K >= 3072 and a last round of 256 x 256 tiles whole or at least 170 / 256
+      full (or at least 1700 tiles): the wide tile, 1.01-1.07x the ring tiles there (`_wide_fits`).
+    - Otherwise M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
       tiles with their measured full-grid rates); the 128 x 256 block as 4 column waves of 128 x 64 with
       fp16 activations, as 2 x 2 waves of 64 x 128 with bf16 ones.
@@ -322,6 +352,8 @@ def select_scaled_mm_config(
     a_bf16 = a_dtype == torch.bfloat16
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
+        if not a_bf16 and _wide_fits(M, N, K):
+            return _TILE_WIDE
         return min(_RING_MODEL if a_bf16 else _RING_MODEL_FP16, key=lambda entry: _ring_time(M, N, *entry))[0]
     min_reread = _BF16_RING_MIN_REREAD if a_bf16 else _RING_MIN_REREAD
     ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
@@ -478,7 +510,7 @@ def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> b
         kernel_s = max(kernel_s, N * K / _WIDEN_WEIGHT_BYTES_PER_S)
     elif splits > 1:
         lead = 0.0
-    elif tuple(tile) == _TILE_RING_128x256_W64:
+    elif tuple(tile) in (_TILE_RING_128x256_W64, _TILE_WIDE):
         lead = _WIDEN_LEAD_W64
     elif tuple(tile) in (_TILE_RING_128x128, _TILE_RING_64x128):
         lead = max(0.0, _WIDEN_LEAD_SMALL * (1.0 - _WIDEN_LEAD_SMALL_K0 / K))

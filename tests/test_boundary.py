@@ -333,7 +333,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto_bf16(1040, 1536, 6144) == ((1, 4, 4, 4, 2, 1), 3)  # 204 tiles x 3 = 612
     assert auto_bf16(1000, 1000, 2560) == ((4, 1, 4, 1, 4, 0), 1)
     assert auto(1040, 1536, 6144)[1] == 2                          # fp16: two per CU at most
-    assert auto(4096, 12288, 3072) == ((1, 4, 4, 8, 4, 1), 1)   # full grids never split
+    assert auto(4096, 12288, 3072) == ((2, 2, 4, 8, 8, 1), 1)   # full grids never split (C3: the wide tile)
     assert auto(16, 14336, 4096)[1] == 1
     # skinny M, long K, fewer than 171 16 x 64 tiles: a streaming tile split to at most one workgroup per CU
     # (the 16 x 32 tile for M <= 12, the 16 x 64 tile with 4 K slices above), each K range 3072 deep or more
@@ -399,8 +399,10 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
 
     bf = torch.bfloat16
     w64 = (1, 4, 4, 8, 4, 1)
-    assert _auto_choice(4096, 12288, 3072, bf) == (w64, 1, True)
-    assert _auto_choice(8192, 8192, 8192, bf) == (w64, 1, True)
+    wide = (2, 2, 4, 8, 8, 1)
+    assert _auto_choice(4096, 12288, 3072, bf) == (wide, 1, True)        # the fp16 pick: the wide tile
+    assert _auto_choice(8192, 8192, 8192, bf) == (wide, 1, True)
+    assert _auto_choice(4096, 12288, 2048, bf) == (w64, 1, True)         # K < 3072: the 128 x 256 block
     assert _auto_choice(4112, 16384, 3072, bf) == (w64, 1, True)         # 0.896 measured
     # 128 x 128: the lead grows with K (1.06-1.09x measured from K = 4608 on, 0.95-1.0x at K <= 3072)
     assert _auto_choice(4096, 4608, 12288, bf) == ((2, 2, 4, 4, 4, 1), 1, True)    # 1.078-1.09x
@@ -418,7 +420,8 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     assert _auto_choice(32, 5120, 25600, bf) == ((2, 2, 4, 2, 2, 1), 6, True)   # 1.16-1.17x
     assert _auto_choice(64, 16384, 4096, bf)[2] is False                         # 64 MB weight: 1.03x, kept
     assert _auto_choice(32, 14336, 4096, bf)[2] is False                         # streaming tile: 0.89x
-    assert _auto_choice(4096, 12288, 3072, torch.float16) == (w64, 1, False)
+    assert _auto_choice(4096, 12288, 3072, torch.float16) == (wide, 1, False)
+    assert widen_first(4096, 12288, 3072, wide, 1)
     # the rule itself: a lead of 17% of the modelled fp16 time against 1.2x the pass (>= 4 us)
     assert widen_first(4096, 12288, 3072, w64, 1) and not widen_first(4096, 12288, 3072, w64, 2)
     assert not widen_first(4096, 12288, 3072, (2, 2, 4, 2, 2, 1), 1)   # no measured lead for that tile
@@ -427,14 +430,15 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
 
 def test_widen_first_only_on_ring_tiles_with_a_measured_lead():
     """Over seeded random shapes: the auto path widens bf16 activations first only onto the ring tiles whose lead
-    was measured (the 128 x 64-wave 128 x 256 block, 128 x 128 and 64 x 128 unsplit, and the 64 x 64 deep ring at
+    was measured (the 128 x 64-wave 128 x 256 block, and the wide tile with its lead, 128 x 128 and 64 x 128
+    unsplit, and the 64 x 64 deep ring at
     M <= 64, split or not), onto the fp16-activation pick, and never for fp16 activations."""
     import numpy as np
 
     from feather_ops.scaled_mm import _auto_choice
 
     rng = np.random.default_rng(3)
-    ring_unsplit = {(1, 4, 4, 8, 4, 1), (2, 2, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1)}
+    ring_unsplit = {(1, 4, 4, 8, 4, 1), (2, 2, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1), (2, 2, 4, 8, 8, 1)}
     for _ in range(400):
         m = int(rng.integers(1, 20000))
         n = int(rng.integers(1, 4000)) * 8
@@ -444,6 +448,25 @@ def test_widen_first_only_on_ring_tiles_with_a_measured_lead():
         if widen:
             assert (tile in ring_unsplit and splits == 1) or (tile == (2, 2, 4, 2, 2, 1) and m <= 64), (m, n, k, tile)
             assert tile == _auto_choice(m, n, k, torch.float16)[0]
+
+
+def test_wide_tile_rule():
+    """The wide tile's regime (fp16 activations): shapes on its grid with K >= 3072 whose last round of 256 tiles is
+    whole or at least 170 / 256 full, or at least 1700 tiles; a single partial round only from K = 4096. One cell
+    each way from the tile sweep."""
+    from feather_ops.scaled_mm import select_scaled_mm_config as pick
+
+    wide = (2, 2, 4, 8, 8, 1)
+    assert pick(4096, 4096, 4096) == wide               # one whole round: 1.067 over the ring
+    assert pick(5376, 5376, 7168) == wide               # 441 tiles, last round 185 / 256: 1.044
+    assert pick(9216, 1280, 5120) == wide               # one round of 180: 1.073
+    assert pick(9216, 18432, 3072) == wide              # 2592 tiles: 1.019
+    assert pick(4096, 3072, 3072) != wide               # one partial round at K = 3072: 0.988
+    assert pick(4096, 4608, 4608) != wide               # 288 tiles: a 32-tile second round, 0.78
+    assert pick(9728, 4096, 4096) != wide               # 608 tiles: 0.972
+    assert pick(4096, 8192, 2048) != wide               # K < 3072
+    assert pick(4112, 4096, 4096) != wide               # off the grid: masked loads
+    assert pick(4096, 12288, 3072, torch.bfloat16) != wide   # bf16 in place: the ring tiles
 
 
 def test_heuristic_returns_instantiated_tiles():
@@ -460,7 +483,8 @@ def test_heuristic_picks_on_representative_cells():
     """The fitted rule's regimes, one cell each (the picks the tile sweep measured best or within noise)."""
     from feather_ops.scaled_mm import select_scaled_mm_config as pick
 
-    assert pick(4096, 12288, 3072) == (1, 4, 4, 8, 4, 1)   # C3: 3 full waves of 128 x 256 (128 x 64 waves)
+    assert pick(4096, 12288, 3072) == (2, 2, 4, 8, 8, 1)   # C3: 3 full rounds of the wide tile
+    assert pick(4112, 12288, 3072) == (1, 4, 4, 8, 4, 1)   # ragged M: 128 x 256 as 128 x 64 waves
     assert pick(4096, 12288, 3072, torch.bfloat16) == (2, 2, 4, 4, 8, 1)   # bf16: 64 x 128 waves
     assert pick(4096, 3072, 3072) == (2, 2, 4, 4, 4, 1)    # C2: one full wave of 128 x 128
     assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
