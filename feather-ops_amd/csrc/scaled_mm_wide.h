@@ -89,13 +89,51 @@ __device__ __forceinline__ uint32_t decode_word(uint32_t w, bool hi) {
     return hi ? decode_word_<kE5M2, true>(w) : decode_word_<kE5M2, false>(w);
 }
 
+// Two fp32 values -> a packed pair of the output type, each rounded to nearest even (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32).
+template <bool kOutBf16>
+__device__ __forceinline__ uint32_t pack_out(float x, float y) {
+    if constexpr (kOutBf16) {
+        using bf16x2v = __bf16 __attribute__((ext_vector_type(2)));
+        using f32x2 = float __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2v));
+    } else {
+        return __builtin_bit_cast(uint32_t, (half2v{static_cast<_Float16>(x), static_cast<_Float16>(y)}));
+    }
+}
+
+// epilogue4's arithmetic (the fp32 product with the scale rounded to the output type, then the bias added in the
+// output precision: the fp32 sum of two fp16 or bf16 values rounded once, as a packed fp16 add rounds it), with
+// packed conversions: 4 multiplies and 2 conversions for 4 outputs, plus 2 packed adds with a bias (fp16).
+template <bool kOutBf16, bool kBias>
+__device__ __forceinline__ u32x2 out4(const f32x4 acc, const f32x4 sc, const u32x2 bias_bits) {
+    uint32_t d[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        d[h] = pack_out<kOutBf16>(acc[2 * h] * sc[2 * h], acc[2 * h + 1] * sc[2 * h + 1]);
+        if constexpr (kBias) {
+            if constexpr (kOutBf16) {
+                const float y0 = __builtin_bit_cast(float, d[h] << 16) + __builtin_bit_cast(float, bias_bits[h] << 16);
+                const float y1 = __builtin_bit_cast(float, d[h] & 0xffff0000u) +
+                                 __builtin_bit_cast(float, bias_bits[h] & 0xffff0000u);
+                d[h] = pack_out<true>(y0, y1);
+            } else {
+                d[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d[h]) + __builtin_bit_cast(half2v, bias_bits[h]));
+            }
+        }
+    }
+    return u32x2{d[0], d[1]};
+}
+
 // A wave's 128 x 128 outputs from its accumulators straight to memory. Lane (g, r) = (lane / 16, lane % 16) holds
 // columns 4g .. 4g + 3 of row r of each 16 x 16 fragment; for fragments j and j + 1, exchanging lane rows 1 and 3
 // of j's values with rows 0 and 2 of j + 1's (v_permlane16_swap, once per dword) leaves lane (g, r) with columns
-// 16 (g & 1) + 8 (g >> 1) .. + 7 of the pair's 32: one 16-byte store. Out-of-range rows and columns (N % 8 == 0,
-// so a piece of 8 columns is wholly in or out) are dropped through the buffer's range check. Scheduling barriers
-// keep the pairs in order, so that only one pair's values are held in VGPRs at a time.
-template <bool kOutBf16, bool kBias, bool kColScale>
+// 16 (g & 1) + 8 (g >> 1) .. + 7 of the pair's 32: one 16-byte store. The lane's offset is computed once; a
+// fragment row's goes in the scalar offset and a pair's in the instruction's. kRagged: rows past M and columns
+// past N (N % 8 == 0, so a piece of 8 columns is wholly in or out) take an out-of-range offset, dropped by the
+// buffer's range check. Scheduling barriers keep the pairs in order, so that only one pair's values are held in
+// VGPRs at a time.
+template <bool kOutBf16, bool kBias, bool kColScale, bool kRagged>
 __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32x4 (&acc)[WideShape::RM][WideShape::RN],
                                                       int row0, int col0, int lane, float scale) {
     constexpr int RM = WideShape::RM;
@@ -112,10 +150,11 @@ __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32
     f32x4 col_scales[RN];
     if constexpr (kColScale) load_col_scales<RN>(p, col0, lane, col_scales);
     const rsrc_t c_rsrc = make_rsrc(p.c, static_cast<uint32_t>(p.M) * static_cast<uint32_t>(p.N) * 2u);
-    const int col_in = 16 * (g & 1) + 8 * (g >> 1);
+    const int col = col0 + 16 * (g & 1) + 8 * (g >> 1);
+    const uint32_t pitch = static_cast<uint32_t>(p.N) * 2u;
+    const uint32_t base = static_cast<uint32_t>(row0 + r16) * pitch + static_cast<uint32_t>(col) * 2u;
 #pragma unroll
     for (int i = 0; i < RM; ++i) {
-        const int row = row0 + 16 * i + r16;
 #pragma unroll
         for (int jp = 0; jp < RN / 2; ++jp) {
             u32x2 y[2];
@@ -124,16 +163,19 @@ __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32
                 const int j = 2 * jp + h;
                 f32x4 sc = f32x4{scale, scale, scale, scale};
                 if constexpr (kColScale) sc = col_scales[j];
-                y[h] = epilogue4<kOutBf16>(acc[i][j], sc, kBias, bias_bits[j]);
+                y[h] = out4<kOutBf16, kBias>(acc[i][j], sc, bias_bits[j]);
             }
             const auto s0 = __builtin_amdgcn_permlane16_swap(y[0][0], y[1][0], false, false);
             const auto s1 = __builtin_amdgcn_permlane16_swap(y[0][1], y[1][1], false, false);
-            const int col = col0 + 32 * jp + col_in;
-            const uint32_t off = row < p.M && col < p.N ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.N) +
-                                                           static_cast<uint32_t>(col)) * 2u
-                                                        : kOob;
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{s0[0], s1[0], s0[1], s1[1]}, c_rsrc, static_cast<int>(off), 0,
-                                                   0);
+            const u32x4 v{s0[0], s1[0], s0[1], s1[1]};
+            if constexpr (kRagged) {
+                const bool ok = row0 + 16 * i + r16 < p.M && col + 32 * jp < p.N;
+                const uint32_t off = ok ? base + static_cast<uint32_t>(16 * i) * pitch + 64u * jp : kOob;
+                __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(off), 0, 0);
+            } else {
+                __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(base + 64u * jp),
+                                                       static_cast<int>(static_cast<uint32_t>(16 * i) * pitch), 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -338,14 +380,14 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
     }
     if (p.col_scale) {
         if (p.bias) {
-            store_wave_tiles_swap<kOutBf16, true, true>(p, acc, row0, col0, lane, scale);
+            store_wave_tiles_swap<kOutBf16, true, true, kRagged>(p, acc, row0, col0, lane, scale);
         } else {
-            store_wave_tiles_swap<kOutBf16, false, true>(p, acc, row0, col0, lane, scale);
+            store_wave_tiles_swap<kOutBf16, false, true, kRagged>(p, acc, row0, col0, lane, scale);
         }
     } else if (p.bias) {
-        store_wave_tiles_swap<kOutBf16, true, false>(p, acc, row0, col0, lane, scale);
+        store_wave_tiles_swap<kOutBf16, true, false, kRagged>(p, acc, row0, col0, lane, scale);
     } else {
-        store_wave_tiles_swap<kOutBf16, false, false>(p, acc, row0, col0, lane, scale);
+        store_wave_tiles_swap<kOutBf16, false, false, kRagged>(p, acc, row0, col0, lane, scale);
     }
 }
 
