@@ -3,7 +3,7 @@
 
 The number the runtime allocates is the code object's `group_segment_fixed_size`; the kernels ask for a
 compile-time function of the tile (the ring kernel: its activation and weight rings, `tiles.ring_slots`,
-shallow or deep; the wide kernel: its 3 + 3 slots of 256 x 64 stages;
+shallow or deep; the wide kernel: its 3 + 3 slots of 256 x 64 activation and 256 or 192 x 64 weight stages;
 the streaming kernel: per-wave activation double buffers plus the K-slice join). A mismatch costs
 occupancy, so it is a bug in the source or the compiler. Same role as the reference's
 `tools/check_lds.py:30-101`, for gfx950: it compiles `csrc/scaled_mm_launch.hip` for one dtype
@@ -36,8 +36,9 @@ def expected_bytes(kernel: str, ints: list[int], bools: list[int] = ()) -> int:
     """LDS bytes the kernel's tile asks for (the kernels' `kLdsBytes`); a ring kernel's fifth template
     flag is its deep-ring variant (the flags after it, such as non-temporal weight loads, leave LDS alone)."""
     if kernel == "wide_kernel":
-        slots_a, slots_b = _tiles().ring_slots(_tiles().WIDE_TILE)
-        return slots_a * 256 * 64 * 2 + slots_b * 256 * 64
+        repeat_n = ints[0]
+        slots_a, slots_b = _tiles().ring_slots((2, 2, 4, 8, repeat_n, 1))
+        return slots_a * 256 * 64 * 2 + slots_b * 32 * repeat_n * 64
     if kernel == "ring_dma_kernel":
         warps_m, warps_n, unroll_k, repeat_m, repeat_n = ints
         deep = bool(bools[4]) if len(bools) >= 5 else False

@@ -154,45 +154,54 @@ __device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
     return u32x4{bf16x2_to_f16x2(v[0]), bf16x2_to_f16x2(v[1]), bf16x2_to_f16x2(v[2]), bf16x2_to_f16x2(v[3])};
 }
 
-// fp32 -> bf16 bits, round to nearest even (subnormals kept, NaN stays NaN): gfx950's v_cvt_pk_bf16_f32,
-// one instruction where the same rounding by hand takes five and a branch for NaN.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
-}
-
+// Two fp32 values -> a packed pair of the output type, each rounded to nearest even, subnormals kept, NaN staying
+// NaN (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32).
 template <bool kOutBf16>
-__device__ __forceinline__ uint32_t round_out(float x) {
+__device__ __forceinline__ uint32_t pack_out(float x, float y) {
     if constexpr (kOutBf16) {
-        return f32_to_bf16_bits(x);
+        using bf16x2v = __bf16 __attribute__((ext_vector_type(2)));
+        using f32x2 = float __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2v));
     } else {
-        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+        return __builtin_bit_cast(uint32_t, (half2v{static_cast<_Float16>(x), static_cast<_Float16>(y)}));
     }
 }
 
-template <bool kOutBf16>
-__device__ __forceinline__ float out_to_f32(uint32_t bits) {
-    if constexpr (kOutBf16) {
-        return __builtin_bit_cast(float, bits << 16);
-    } else {
-        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+// The epilogue's arithmetic for 4 consecutive columns of one row (naive.py:29-40): the fp32 product with the
+// scale, rounded to the output type, then the bias added in the output precision (the fp32 sum of two fp16 or
+// bf16 values rounded once, as a packed fp16 add rounds it), with packed conversions: 4 multiplies and 2
+// conversions for 4 outputs, plus 2 packed adds with a bias (fp16). The product is rounded to fp32 first, as
+// the reference computes it: a multiply whose result goes straight to an fp16 conversion compiles to
+// v_fma_mixlo_f16, one rounding of the exact product, which differs from that by one fp16 ulp now and then;
+// the packed conversion keeps the two roundings.
+template <bool kOutBf16, bool kBias>
+__device__ __forceinline__ u32x2 out4(const f32x4 acc, const f32x4 sc, const u32x2 bias_bits) {
+    uint32_t d[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        d[h] = pack_out<kOutBf16>(acc[2 * h] * sc[2 * h], acc[2 * h + 1] * sc[2 * h + 1]);
+        if constexpr (kBias) {
+            if constexpr (kOutBf16) {
+                const float y0 = __builtin_bit_cast(float, d[h] << 16) + __builtin_bit_cast(float, bias_bits[h] << 16);
+                const float y1 = __builtin_bit_cast(float, d[h] & 0xffff0000u) +
+                                 __builtin_bit_cast(float, bias_bits[h] & 0xffff0000u);
+                d[h] = pack_out<true>(y0, y1);
+            } else {
+                // The element goes through a scalar first: this hipcc's __builtin_bit_cast of an ext-vector
+                // element lvalue (bias_bits[h] itself) reads element 0 whatever h is.
+                const uint32_t bias_pair = bias_bits[h];
+                d[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d[h]) + __builtin_bit_cast(half2v, bias_pair));
+            }
+        }
     }
+    return u32x2{d[0], d[1]};
 }
 
 // acc (4 consecutive columns of one row) -> scaled, rounded, biased output bits, packed for one 8-byte store.
 // scale: the 4 columns' scales (all equal for a per-tensor scale).
 template <bool kOutBf16>
 __device__ __forceinline__ u32x2 epilogue4(const f32x4 acc, f32x4 scale, bool has_bias, u32x2 bias_bits) {
-    uint32_t o[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        uint32_t y = round_out<kOutBf16>(acc[v] * scale[v]);
-        if (has_bias) {
-            const uint32_t bb = (bias_bits[v / 2] >> (16 * (v % 2))) & 0xffffu;
-            y = round_out<kOutBf16>(out_to_f32<kOutBf16>(y) + out_to_f32<kOutBf16>(bb));
-        }
-        o[v] = y;
-    }
-    return u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    return has_bias ? out4<kOutBf16, true>(acc, scale, bias_bits) : out4<kOutBf16, false>(acc, scale, bias_bits);
 }
 
 __device__ __forceinline__ f32x4 mfma16(half8 w, half8 x, f32x4 acc) {

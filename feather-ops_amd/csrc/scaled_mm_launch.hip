@@ -58,7 +58,7 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
     }
     if constexpr (PF != 0 && is_wide_tile<WM, WN, U, RM, RN>()) {
         // One workgroup per CU, one wave per SIMD: the software-pipelined wide kernel.
-        using S = WideShape;
+        using S = WideShape<RN>;
         const int64_t tiles = ((p.M + S::kBM - 1) / S::kBM) * static_cast<int64_t>((p.N + S::kBN - 1) / S::kBN);
         const dim3 grid(static_cast<uint32_t>(tiles * p.splits));
         // M, N or K off the tile grid: the instantiation that masks every load per lane.
@@ -66,14 +66,14 @@ bool try_tile(const TileQuery& t, const Params& p, hipStream_t stream) {
         const auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(S::kThreads), 0, stream, p); };
         if (p.splits > 1) {
             if (ragged) {
-                go(wide_kernel<kE5M2, kABf16, kOutBf16, true, true>);
+                go(wide_kernel<RN, kE5M2, kABf16, kOutBf16, true, true>);
             } else {
-                go(wide_kernel<kE5M2, kABf16, kOutBf16, true, false>);
+                go(wide_kernel<RN, kE5M2, kABf16, kOutBf16, true, false>);
             }
         } else if (ragged) {
-            go(wide_kernel<kE5M2, kABf16, kOutBf16, false, true>);
+            go(wide_kernel<RN, kE5M2, kABf16, kOutBf16, false, true>);
         } else {
-            go(wide_kernel<kE5M2, kABf16, kOutBf16, false, false>);
+            go(wide_kernel<RN, kE5M2, kABf16, kOutBf16, false, false>);
         }
     } else if constexpr (PF != 0) {
         using S = DmaShape<WM, WN, U, RM, RN>;

@@ -38,39 +38,51 @@
 
 namespace feather {
 
+// RN_: 16-column weight fragments per wave, 8 (256 x 256 tiles) or 6 (256 x 192 tiles: 4 waves of 128 x 96, a
+// 132 KiB ring; e.g. one tile per CU on a 4096 x 3072 output).
+template <int RN_>
 struct WideShape {
     static constexpr int kWaves = 4;
     static constexpr int kThreads = kWave * kWaves;
     static constexpr int RM = 8;                           // 16-row activation fragments per wave
-    static constexpr int RN = 8;                           // 16-column weight fragments per wave
+    static constexpr int RN = RN_;                         // 16-column weight fragments per wave
     static constexpr int kBM = 2 * 16 * RM;                // 256
-    static constexpr int kBN = 2 * 16 * RN;                // 256
+    static constexpr int kBN = 2 * 16 * RN;                // 256 or 192
     static constexpr int kUnitsPerRow = 8;                 // a stage's activation row: 64 k x 2 bytes = 8 x 16 B
     static constexpr int kABytes = kBM * kUnitsPerRow * 16;   // 32 KiB, [row][8 units], units XOR-swizzled
-    static constexpr int kBBytes = 4 * kBN * 16;              // 16 KiB, [chunk][col][16 bytes]
+    static constexpr int kBBytes = 4 * kBN * 16;              // 16 or 12 KiB, [chunk][col][16 bytes]
     static constexpr int kStageBytes = kABytes + kBBytes;
     static constexpr int kSlots = 3;
-    static constexpr int kLdsBytes = kSlots * kStageBytes;    // 144 KiB: one workgroup per CU
+    static constexpr int kLdsBytes = kSlots * kStageBytes;    // 144 or 132 KiB: one workgroup per CU
     static constexpr int kAInstr = kABytes / 1024 / kWaves;   // 8 direct loads of 1 KiB per wave and stage
-    static constexpr int kBInstr = kBBytes / 1024 / kWaves;   // 4
+    static constexpr int kBInstr = kBBytes / 1024 / kWaves;   // 4 or 3
     static constexpr int kLoadsPerStage = kAInstr + kBInstr;
+    static constexpr int kMfmas = RM * RN;                    // MFMAs of one k half
     // Direct loads of stage t + 3 issued in the second half of stage t (every kEarlyStep MFMAs from kEarlyAt); the
     // rest of them in the first half of stage t + 1 (every kLateStep MFMAs from kLateAt). Of the placements
-    // measured (bursts, and spreads over one half or both), this one took the fewest clocks per stage.
-    static constexpr int kLoadsEarly = 8;
-    static constexpr int kEarlyAt = 24;
-    static constexpr int kEarlyStep = 5;
+    // measured (bursts, and spreads over one half or both), these took the fewest clocks per stage.
+    static constexpr int kLoadsEarly = RN == 8 ? 8 : 7;
+    static constexpr int kEarlyAt = RN == 8 ? 24 : 16;
+    static constexpr int kEarlyStep = RN == 8 ? 5 : 4;
     static constexpr int kLateAt = 5;
-    static constexpr int kLateStep = 14;
-    static_assert(kEarlyAt >= 8 && kEarlyAt + kEarlyStep * (kLoadsEarly - 1) < RM * RN, "early loads fit");
-    static_assert(kLateAt + kLateStep * (kLoadsPerStage - kLoadsEarly - 1) < RM * RN, "late loads fit");
+    static constexpr int kLateStep = RN == 8 ? 14 : 11;
+    // Second k half: the weights of stage t + 1 are read at MFMAs [8, 8 + RN), its first-half activations at
+    // [8 + RN, 8 + RN + RM), and its first-half weights decoded two dwords per MFMA from kDecode0; the first half
+    // decodes the second-half weights one dword per MFMA from kDecode1.
+    static constexpr int kDecode0 = kMfmas - 2 * RN;
+    static constexpr int kDecode1 = kMfmas - 4 * RN;
+    static_assert(RN == 8 || RN == 6, "the two wide tiles");
+    static_assert(kEarlyAt >= 8 && kEarlyAt + kEarlyStep * (kLoadsEarly - 1) < kMfmas, "early loads fit");
+    static_assert(kLateAt + kLateStep * (kLoadsPerStage - kLoadsEarly - 1) < kMfmas, "late loads fit");
+    static_assert(8 + RN + RM <= kDecode0, "operand reads precede the decode they feed");
     static_assert(2 * kLoadsPerStage < 64, "vmcnt range");
 };
 
-// The tile the launcher runs on the wide kernel: (warps_m, warps_n, unroll_k, repeat_m, repeat_n) = (2, 2, 4, 8, 8).
+// The tiles the launcher runs on the wide kernel: (warps_m, warps_n, unroll_k, repeat_m, repeat_n) = (2, 2, 4, 8, 8)
+// and (2, 2, 4, 8, 6).
 template <int WM, int WN, int U, int RM, int RN>
 constexpr bool is_wide_tile() {
-    return WM == 2 && WN == 2 && U == 4 && RM == WideShape::RM && RN == WideShape::RN;
+    return WM == 2 && WN == 2 && U == 4 && RM == 8 && (RN == 8 || RN == 6);
 }
 
 // One fp16 dword (two k values) of a weight fragment from one dword of 4 codes: its low (kHi = false) or high two
@@ -89,42 +101,6 @@ __device__ __forceinline__ uint32_t decode_word(uint32_t w, bool hi) {
     return hi ? decode_word_<kE5M2, true>(w) : decode_word_<kE5M2, false>(w);
 }
 
-// Two fp32 values -> a packed pair of the output type, each rounded to nearest even (v_cvt_pk_f16_f32 /
-// v_cvt_pk_bf16_f32).
-template <bool kOutBf16>
-__device__ __forceinline__ uint32_t pack_out(float x, float y) {
-    if constexpr (kOutBf16) {
-        using bf16x2v = __bf16 __attribute__((ext_vector_type(2)));
-        using f32x2 = float __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2v));
-    } else {
-        return __builtin_bit_cast(uint32_t, (half2v{static_cast<_Float16>(x), static_cast<_Float16>(y)}));
-    }
-}
-
-// epilogue4's arithmetic (the fp32 product with the scale rounded to the output type, then the bias added in the
-// output precision: the fp32 sum of two fp16 or bf16 values rounded once, as a packed fp16 add rounds it), with
-// packed conversions: 4 multiplies and 2 conversions for 4 outputs, plus 2 packed adds with a bias (fp16).
-template <bool kOutBf16, bool kBias>
-__device__ __forceinline__ u32x2 out4(const f32x4 acc, const f32x4 sc, const u32x2 bias_bits) {
-    uint32_t d[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        d[h] = pack_out<kOutBf16>(acc[2 * h] * sc[2 * h], acc[2 * h + 1] * sc[2 * h + 1]);
-        if constexpr (kBias) {
-            if constexpr (kOutBf16) {
-                const float y0 = __builtin_bit_cast(float, d[h] << 16) + __builtin_bit_cast(float, bias_bits[h] << 16);
-                const float y1 = __builtin_bit_cast(float, d[h] & 0xffff0000u) +
-                                 __builtin_bit_cast(float, bias_bits[h] & 0xffff0000u);
-                d[h] = pack_out<true>(y0, y1);
-            } else {
-                d[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, d[h]) + __builtin_bit_cast(half2v, bias_bits[h]));
-            }
-        }
-    }
-    return u32x2{d[0], d[1]};
-}
-
 // A wave's 128 x 128 outputs from its accumulators straight to memory. Lane (g, r) = (lane / 16, lane % 16) holds
 // columns 4g .. 4g + 3 of row r of each 16 x 16 fragment; for fragments j and j + 1, exchanging lane rows 1 and 3
 // of j's values with rows 0 and 2 of j + 1's (v_permlane16_swap, once per dword) leaves lane (g, r) with columns
@@ -133,11 +109,10 @@ __device__ __forceinline__ u32x2 out4(const f32x4 acc, const f32x4 sc, const u32
 // past N (N % 8 == 0, so a piece of 8 columns is wholly in or out) take an out-of-range offset, dropped by the
 // buffer's range check. Scheduling barriers keep the pairs in order, so that only one pair's values are held in
 // VGPRs at a time.
-template <bool kOutBf16, bool kBias, bool kColScale, bool kRagged>
-__device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32x4 (&acc)[WideShape::RM][WideShape::RN],
-                                                      int row0, int col0, int lane, float scale) {
-    constexpr int RM = WideShape::RM;
-    constexpr int RN = WideShape::RN;
+template <int RM, int RN, bool kOutBf16, bool kBias, bool kColScale, bool kRagged>
+__device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32x4 (&acc)[RM][RN], int row0, int col0,
+                                                      int lane, float scale) {
+    static_assert(RN % 2 == 0, "fragment pairs");
     const int g = lane >> 4;
     const int r16 = lane & 15;
     u32x2 bias_bits[RN];
@@ -181,13 +156,13 @@ __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32
     }
 }
 
-// kRagged: M % 256, N % 256 or K % 64 is not zero. Then every direct load masks its lanes (rows past M, columns
+// kRagged: M % 256, N % kBN or K % 64 is not zero. Then every direct load masks its lanes (rows past M, columns
 // past N and chunks past K read zeros). Otherwise every load is whole and in range: the per-lane offsets are fixed
 // and the tile and stage go in the scalar offset.
-template <bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK, bool kRagged>
-__global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void wide_kernel(
+template <int RN_, bool kE5M2, bool kABf16, bool kOutBf16, bool kSplitK, bool kRagged>
+__global__ __launch_bounds__(WideShape<RN_>::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void wide_kernel(
     const Params p) {
-    using S = WideShape;
+    using S = WideShape<RN_>;
     constexpr int RM = S::RM;
     constexpr int RN = S::RN;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S::kLdsBytes];
@@ -220,9 +195,10 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
     const float scale = load_scale(p);
 
     // Direct loads (the ring kernel's layout): load d < 8 of this wave fills 1 KiB of a slot's activations (8 rows
-    // of 8 units: row (wave + 4d) * 8 + lane / 8 of the tile, physical unit lane % 8), load 8 + i fills chunk i of the
-    // slot's weights for 64 of its 256 columns (column wave * 64 + lane). Per-lane offsets within the tile and
-    // stage; the unit's k chunk (the same for every d: the swizzle key depends on the row mod 16 only).
+    // of 8 units: row (wave + 4d) * 8 + lane / 8 of the tile, physical unit lane % 8), load 8 + i fills the slot's
+    // weight pieces e * 64 + lane, e = wave + 4i, of its [4 chunks][kBN columns] (kBN a multiple of 64, so one
+    // load covers 64 columns of one chunk). Per-lane offsets within the tile and stage; the unit's k chunk (the
+    // same for every d: the swizzle key depends on the row mod 16 only).
     uint32_t a_lane_off[S::kAInstr];
     int a_chunk = 0;
 #pragma unroll
@@ -234,11 +210,21 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
         a_lane_off[d] = (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>(u * 8)) * 2u;
     }
     const int a_row_in = lane / S::kUnitsPerRow + wave * S::kUnitsPerRow;   // + 32 d: the row of load d
-    const int b_col_in = wave * kWave + lane;
+    static_assert(S::kBN % kWave == 0, "a weight load covers one chunk");
+    int b_col_in[S::kBInstr], b_chunk[S::kBInstr];
     uint32_t b_lane_off[S::kBInstr];
 #pragma unroll
     for (int i = 0; i < S::kBInstr; ++i) {
-        b_lane_off[i] = (static_cast<uint32_t>(i) * static_cast<uint32_t>(p.N) + static_cast<uint32_t>(b_col_in)) * 16u;
+        if constexpr (S::kBN == S::kWaves * kWave) {
+            b_chunk[i] = i;   // load i: chunk i, column wave * 64 + lane
+            b_col_in[i] = wave * kWave + lane;
+        } else {
+            const int e = wave + i * S::kWaves;
+            b_chunk[i] = e * kWave / S::kBN;
+            b_col_in[i] = e * kWave % S::kBN + lane;
+        }
+        b_lane_off[i] = (static_cast<uint32_t>(b_chunk[i]) * static_cast<uint32_t>(p.N) +
+                         static_cast<uint32_t>(b_col_in[i])) * 16u;
     }
     const uint32_t a_tile_off = static_cast<uint32_t>(m0) * static_cast<uint32_t>(p.K) * 2u;
     const uint32_t b_tile_off = static_cast<uint32_t>(n0) * 16u;
@@ -263,7 +249,7 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
             const int i = d - S::kAInstr;
             uint8_t* dst = lds + slot + S::kABytes + (wave + i * S::kWaves) * 1024;
             if constexpr (kRagged) {
-                const bool ok = n0 + b_col_in < p.N && i < k_chunks - 4 * stage;
+                const bool ok = n0 + b_col_in[i] < p.N && b_chunk[i] < k_chunks - 4 * stage;
                 dma16(live ? b_rsrc : null_rsrc, dst, ok ? b_tile_off + b_lane_off[i] : kOob,
                       live ? static_cast<uint32_t>(stage) * b_stage_stride : 0u);
             } else {
@@ -319,15 +305,15 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
     for (int t = 0; t < stages; ++t) {
         // First k half.
 #pragma unroll
-        for (int m = 0; m < RM * RN; ++m) {
+        for (int m = 0; m < S::kMfmas; ++m) {
             const int i = m / RN;
             const int jj = m % RN;
             const int j = (i & 1) ? RN - 1 - jj : jj;
             acc[i][j] = mfma16(__builtin_bit_cast(half8, u32x4{w0[j][0], w0[j][1], w0[j][2], w0[j][3]}), as_f16(x0[i]),
                                acc[i][j]);
             if (jj == 0) x1[i] = read16(cur + a_rd1 + i * 2048);
-            if (m >= 32) {
-                const int q = m - 32;  // 32 dwords of second-half weights, one per MFMA
+            if (m >= S::kDecode1) {
+                const int q = m - S::kDecode1;  // 4 RN dwords of second-half weights, one per MFMA
                 w1[q / 4][q % 4] = decode_word<kE5M2>(braw[q / 4][2 + (q % 4) / 2], q & 1);
             }
             if (m >= S::kLateAt && (m - S::kLateAt) % S::kLateStep == 0 &&
@@ -338,7 +324,7 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
         }
         // Second k half.
 #pragma unroll
-        for (int m = 0; m < RM * RN; ++m) {
+        for (int m = 0; m < S::kMfmas; ++m) {
             const int i = m / RN;
             const int jj = m % RN;
             const int j = (i & 1) ? RN - 1 - jj : jj;
@@ -352,14 +338,14 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(S::kLoadsPerStage));
                 barrier_only();
             }
-            if (m >= 8 && m < 16) braw[m - 8] = read16(nxt + b_rd + (m - 8) * 256);
-            if (m >= 16 && m < 24) x0[m - 16] = read16(nxt + a_rd0 + (m - 16) * 2048);
+            if (m >= 8 && m < 8 + RN) braw[m - 8] = read16(nxt + b_rd + (m - 8) * 256);
+            if (m >= 8 + RN && m < 8 + RN + RM) x0[m - 8 - RN] = read16(nxt + a_rd0 + (m - 8 - RN) * 2048);
             if (m >= S::kEarlyAt && (m - S::kEarlyAt) % S::kEarlyStep == 0 &&
                 (m - S::kEarlyAt) / S::kEarlyStep < S::kLoadsEarly) {
                 dma((m - S::kEarlyAt) / S::kEarlyStep, t + 3, cur);
             }
-            if (m >= 48) {
-                const int q = 2 * (m - 48);  // 32 dwords of stage t + 1's first-half weights, two per MFMA
+            if (m >= S::kDecode0) {
+                const int q = 2 * (m - S::kDecode0);  // 4 RN dwords of stage t + 1's first-half weights, two per MFMA
                 w0[q / 4][q % 4] = decode_word<kE5M2>(braw[q / 4][(q % 4) / 2], q & 1);
                 w0[(q + 1) / 4][(q + 1) % 4] = decode_word<kE5M2>(braw[(q + 1) / 4][((q + 1) % 4) / 2], (q + 1) & 1);
             }
@@ -380,14 +366,14 @@ __global__ __launch_bounds__(WideShape::kThreads) __attribute__((amdgpu_waves_pe
     }
     if (p.col_scale) {
         if (p.bias) {
-            store_wave_tiles_swap<kOutBf16, true, true, kRagged>(p, acc, row0, col0, lane, scale);
+            store_wave_tiles_swap<RM, RN, kOutBf16, true, true, kRagged>(p, acc, row0, col0, lane, scale);
         } else {
-            store_wave_tiles_swap<kOutBf16, false, true, kRagged>(p, acc, row0, col0, lane, scale);
+            store_wave_tiles_swap<RM, RN, kOutBf16, false, true, kRagged>(p, acc, row0, col0, lane, scale);
         }
     } else if (p.bias) {
-        store_wave_tiles_swap<kOutBf16, true, false, kRagged>(p, acc, row0, col0, lane, scale);
+        store_wave_tiles_swap<RM, RN, kOutBf16, true, false, kRagged>(p, acc, row0, col0, lane, scale);
     } else {
-        store_wave_tiles_swap<kOutBf16, false, false, kRagged>(p, acc, row0, col0, lane, scale);
+        store_wave_tiles_swap<RM, RN, kOutBf16, false, false, kRagged>(p, acc, row0, col0, lane, scale);
     }
 }
 

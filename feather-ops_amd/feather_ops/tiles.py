@@ -41,6 +41,7 @@ SCALED_MM_TILES = [
     (1, 4, 4, 4, 2, 1),  # 64 x 128
     (2, 2, 4, 2, 2, 1),  # 64 x 64
     (2, 2, 4, 8, 8, 1),  # 256 x 256, 4 waves of 128 x 128, one block per CU: the software-pipelined wide kernel
+    (2, 2, 4, 8, 6, 1),  # 256 x 192, 4 waves of 128 x 96, one block per CU: the wide kernel
     # streaming split-K (prefetch = 0)
     (4, 1, 4, 1, 4, 0),  # 16 x 64, 4 K slices
     (4, 1, 8, 1, 4, 0),  # 16 x 64, 4 K slices, 128-deep steps
@@ -66,18 +67,20 @@ def gemm_block_sizes(tile: tuple[int, ...]) -> tuple[int, int, int]:
 
 
 WIDE_TILE = (2, 2, 4, 8, 8, 1)
+WIDE_TILE_192 = (2, 2, 4, 8, 6, 1)
 
 
 def is_wide(tile: tuple[int, ...]) -> bool:
-    """Whether a `prefetch = 1` tile runs on the wide kernel (256 x 256, 4 waves of 128 x 128, one workgroup per
-    CU, 512 registers per wave) rather than the ring kernel: `(2, 2, 4, 8, 8, 1)`."""
-    return tuple(tile[:6]) == WIDE_TILE
+    """Whether a `prefetch = 1` tile runs on the wide kernel (4 waves of 128 x 16 repeat_n, one workgroup per CU,
+    512 registers per wave) rather than the ring kernel: `(2, 2, 4, 8, 8, 1)` (256 x 256) and `(2, 2, 4, 8, 6, 1)`
+    (256 x 192)."""
+    return tuple(tile[:6]) in (WIDE_TILE, WIDE_TILE_192)
 
 
 def ring_slots(tile: tuple[int, ...], deep: bool = False) -> tuple[int, int]:
     """(activation, weight) LDS ring slots of a `prefetch = 1` tile, the rule the kernel applies.
 
-    The wide tile (`is_wide`) keeps 3 of each. Blocks of up to 4 waves keep 2 activation slots within an 80 KiB budget, bigger blocks 3 within
+    The wide tiles (`is_wide`) keep 3 of each. Blocks of up to 4 waves keep 2 activation slots within an 80 KiB budget, bigger blocks 3 within
     160 KiB; the weight ring gets one more slot when that fits the budget and the tile already runs at
     most two blocks per CU (8-wave blocks: always when it fits). `deep`: the deep-ring variant of a
     64-row tile (3 and 4 slots), which the launcher takes for grids whose blocks are all resident at once
@@ -88,7 +91,7 @@ def ring_slots(tile: tuple[int, ...], deep: bool = False) -> tuple[int, int]:
             raise ValueError(f"the deep ring is for 64-row tiles: {tile}")
         return 3, 4
     if is_wide(tile):
-        return 3, 3  # the wide kernel: 3 x (32 + 16) KiB, one workgroup per CU
+        return 3, 3  # the wide kernel: 3 x (32 + 16 or 12) KiB, one workgroup per CU
     warps_m, warps_n, unroll_k, repeat_m, repeat_n = tile[:5]
     waves = warps_m * warps_n
     a_bytes = 16 * warps_m * repeat_m * unroll_k * 32
