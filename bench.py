@@ -13,9 +13,10 @@ time per step.
 
 Also reported: the skinny HBM-bound cell C4 (A fp16 [16, 4096] x W e5m2 [14336, 4096]) as GB/s of
 algorithmic bytes, timed over a HIP graph of launches that rotate over 8 distinct weight copies (8 x
-58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2, the C3 shape
-with e4m3fn weights, the C3 shape with bf16 activations through the auto path (which widens them in a pass
-of their own there and runs the fp16-activation kernel; the in-place widening's time beside it), two
+58.7 MB > the 256 MB MALL, so each launch streams its weight from HBM), the bf16 cell C2 through the auto
+path (with the in-place widening's time and the fp16-activation kernel's beside it), the C3 shape with
+e4m3fn weights, the C3 shape with bf16 activations through the auto path (which widens them in a pass of
+their own there and runs the fp16-activation kernel; the in-place widening's time beside it), two
 split-K cells with the unsplit tile beside each, and `cpu_baseline`: the
 reference's CPU path (naive.py's semantics as torch CPU calls with fp32 accumulation) on C1, the
 CPU configuration, on the host's cores.
@@ -491,9 +492,10 @@ def main() -> int:
     c3 = time_c3(args.steps, args.warmup, rounds)
     sec = not args.no_secondary
     c4 = time_c4(rounds) if sec else None
-    c2 = time_square_cell(4096, 3072, 3072, "bf16", "e5m2", 50, 10, rounds) if sec else None
-    # the same shape with fp16 activations: separates the bf16 widening's cost from the grid's (one round of
-    # 768 128 x 128 blocks)
+    # C2 through the auto path (the widening pass, then the fp16-activation kernel: one round of 256 x 192
+    # tiles), the in-place widening on the bf16 pick beside it
+    c2 = time_bf16_auto_cell(4096, 3072, 3072, 50, 10, rounds) if sec else None
+    # the same shape with fp16 activations: separates the bf16 widening's cost from the kernel's
     c2h = time_square_cell(4096, 3072, 3072, "fp16", "e5m2", 50, 10, rounds) if sec else None
     e4 = time_square_cell(4096, 3072, 12288, "fp16", "e4m3fn", 20, 10, rounds) if sec else None
     bw = time_bf16_auto_cell(4096, 3072, 12288, 20, 10, rounds) if sec else None

@@ -60,12 +60,14 @@ struct WideShape {
     static constexpr int kMfmas = RM * RN;                    // MFMAs of one k half
     // Direct loads of stage t + 3 issued in the second half of stage t (every kEarlyStep MFMAs from kEarlyAt); the
     // rest of them in the first half of stage t + 1 (every kLateStep MFMAs from kLateAt). Of the placements
-    // measured (bursts, and spreads over one half or both), these took the fewest clocks per stage.
-    static constexpr int kLoadsEarly = RN == 8 ? 8 : 7;
-    static constexpr int kEarlyAt = RN == 8 ? 24 : 16;
-    static constexpr int kEarlyStep = RN == 8 ? 5 : 4;
-    static constexpr int kLateAt = 5;
-    static constexpr int kLateStep = RN == 8 ? 14 : 11;
+    // measured (bursts, and spreads over one half or both), these took the fewest clocks per stage. For the
+    // 256 x 192 tile the spreads over both halves measured within 1% of each other on 4096 x 3072 x 3072 and
+    // 4096 x 3072 x 12288 (5 early from MFMA 24 and 6 late from MFMA 4 the fastest); all 11 in one half, 30% slower.
+    static constexpr int kLoadsEarly = RN == 8 ? 8 : 5;
+    static constexpr int kEarlyAt = 24;
+    static constexpr int kEarlyStep = 5;
+    static constexpr int kLateAt = RN == 8 ? 5 : 4;
+    static constexpr int kLateStep = RN == 8 ? 14 : 8;
     // Second k half: the weights of stage t + 1 are read at MFMAs [8, 8 + RN), its first-half activations at
     // [8 + RN, 8 + RN + RM), and its first-half weights decoded two dwords per MFMA from kDecode0; the first half
     // decodes the second-half weights one dword per MFMA from kDecode1.

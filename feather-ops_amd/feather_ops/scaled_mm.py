@@ -33,8 +33,10 @@ _TILE_RING_128x256 = (2, 2, 4, 4, 8, 1)
 # tile) it measured even.
 _TILE_RING_128x256_W64 = (1, 4, 4, 8, 4, 1)
 _TILE_RING_256x256 = (4, 2, 4, 4, 8, 1)
-# The wide kernel's tile: 256 x 256 on one workgroup per CU, 4 waves of 128 x 128 (tiles.py `is_wide`).
+# The wide kernel's tiles: 256 x 256 and 256 x 192 on one workgroup per CU, 4 waves of 128 x 128 or 128 x 96
+# (tiles.py `is_wide`).
 _TILE_WIDE = (2, 2, 4, 8, 8, 1)
+_TILE_WIDE_192 = (2, 2, 4, 8, 6, 1)
 _TILE_RING_128x128 = (2, 2, 4, 4, 4, 1)
 _TILE_RING_64x128 = (1, 4, 4, 4, 2, 1)
 _TILE_RING_64x64 = (2, 2, 4, 2, 2, 1)
@@ -90,6 +92,23 @@ def _wide_fits(M: int, N: int, K: int) -> bool:
     if tiles < _CUS and K < _WIDE_SINGLE_ROUND_MIN_K:
         return False
     return tiles % _CUS == 0 or tiles % _CUS >= _WIDE_MIN_LAST_ROUND or tiles >= _WIDE_MANY_TILES
+
+
+# The 256 x 192 wide tile (fp16 activations; bf16 ones widened first): when its tiles make one round at least
+# 205 / 256 full, with K >= 3072 (a multiple of 64), any M and N (ragged ones on its masked path). Measured with
+# the tile sweep on the 76 large-grid cells: it takes 6 of them, each faster than every other tile there (4096 x
+# 3072 x 3072 1.114x, 4096 x 3072 x 12288 1.097x, 6416 x 1536 x 6144 1.052x, 9232 x 1024 x 5120 1.051x, 9216 x
+# 1280 x 5120 1.023x, 4112 x 2560 x 6912 1.022x); past one round it loses (272 tiles: 0.60x; 352: 0.66-0.69x),
+# as it does below 3072 deep (1024 x 10240 x 1280, 216 tiles: 0.96x). Against the 256 x 256 tile it fills 4/3
+# as many CUs where that one's grid is a partial round.
+_WIDE_192_MIN_TILES = 205
+
+
+def _wide192_fits(M: int, N: int, K: int) -> bool:
+    """Whether the fp16-activation heuristic takes the 256 x 192 wide tile (see _WIDE_192_MIN_TILES)."""
+    if K % 64 or K < _WIDE_MIN_K:
+        return False
+    return _WIDE_192_MIN_TILES <= -(-M // 256) * -(-N // 192) <= _CUS
 
 
 # Split-K applies from this K (64 stages of 64) and keeps at least 16 stages per split.
@@ -305,9 +324,12 @@ def select_scaled_mm_config(
     Fitted on MI355X with the tile sweep over the benchmark grid (112 cells, every tile and split count;
     with `select_scaled_mm_splits` the pick is within 0.7% of the best candidate in geometric mean) and
     extra cells where the grid had few:
-    - M > 64 and at least one CU's worth of 128 x 128 tiles, fp16 activations, on the wide tile's grid (M and N
-      multiples of 256, K of 64) with K >= 3072 and a last round of 256 x 256 tiles whole or at least 170 / 256
-      full (or at least 1700 tiles): the wide tile, 1.01-1.07x the ring tiles there (`_wide_fits`).
+    - M > 64 and at least one CU's worth of 128 x 128 tiles, fp16 activations, K >= 3072 (a multiple of 64), and
+      one round of 256 x 192 tiles at least 205 / 256 full: the 256 x 192 wide tile, 1.02-1.11x the best other
+      tile there (`_wide192_fits`).
+    - Else the same, on the wide tile's grid (M and N multiples of 256, K of 64) with K >= 3072 and a last round
+      of 256 x 256 tiles whole or at least 170 / 256 full (or at least 1700 tiles): the 256 x 256 wide tile,
+      1.01-1.07x the ring tiles there (`_wide_fits`).
     - Otherwise M > 64 and at least one CU's worth of 128 x 128 tiles: the ring tile whose whole waves of resident
       blocks finish first (a wave-quantization model over 128 x 256, 256 x 256, 128 x 128 and 64 x 128
       tiles with their measured full-grid rates); the 128 x 256 block as 4 column waves of 128 x 64 with
@@ -352,6 +374,8 @@ def select_scaled_mm_config(
     a_bf16 = a_dtype == torch.bfloat16
     tiles_128 = _blocks(M, N, _TILE_RING_128x128)
     if M > 64 and tiles_128 >= _CUS:
+        if not a_bf16 and _wide192_fits(M, N, K):
+            return _TILE_WIDE_192
         if not a_bf16 and _wide_fits(M, N, K):
             return _TILE_WIDE
         return min(_RING_MODEL if a_bf16 else _RING_MODEL_FP16, key=lambda entry: _ring_time(M, N, *entry))[0]
@@ -510,7 +534,7 @@ def widen_first(M: int, N: int, K: int, tile: tuple[int, ...], splits: int) -> b
         kernel_s = max(kernel_s, N * K / _WIDEN_WEIGHT_BYTES_PER_S)
     elif splits > 1:
         lead = 0.0
-    elif tuple(tile) in (_TILE_RING_128x256_W64, _TILE_WIDE):
+    elif tuple(tile) in (_TILE_RING_128x256_W64, _TILE_WIDE, _TILE_WIDE_192):
         lead = _WIDEN_LEAD_W64
     elif tuple(tile) in (_TILE_RING_128x128, _TILE_RING_64x128):
         lead = max(0.0, _WIDEN_LEAD_SMALL * (1.0 - _WIDEN_LEAD_SMALL_K0 / K))

@@ -407,7 +407,8 @@ def test_bf16_activations_widen_first_only_where_the_fp16_kernel_repays_it():
     # 128 x 128: the lead grows with K (1.06-1.09x measured from K = 4608 on, 0.95-1.0x at K <= 3072)
     assert _auto_choice(4096, 4608, 12288, bf) == ((2, 2, 4, 4, 4, 1), 1, True)    # 1.078-1.09x
     assert _auto_choice(4608, 4096, 16384, bf) == ((2, 2, 4, 4, 4, 1), 1, True)    # 1.087-1.089x
-    assert _auto_choice(4096, 3072, 3072, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C2: 1.057 if widened
+    # C2: the fp16 pick is the 256 x 192 wide tile (57.5 us), widened first (8.8 us) against 69.8 us in place
+    assert _auto_choice(4096, 3072, 3072, bf) == ((2, 2, 4, 8, 6, 1), 1, True)
     assert _auto_choice(4097, 5120, 2560, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # C5's largest: 1.025
     assert _auto_choice(6416, 1536, 6144, bf) == ((2, 2, 4, 4, 4, 1), 1, False)   # narrow weight: 1.158
     assert _auto_choice(9232, 1024, 5120, bf)[2] is False
@@ -438,7 +439,7 @@ def test_widen_first_only_on_ring_tiles_with_a_measured_lead():
     from feather_ops.scaled_mm import _auto_choice
 
     rng = np.random.default_rng(3)
-    ring_unsplit = {(1, 4, 4, 8, 4, 1), (2, 2, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1), (2, 2, 4, 8, 8, 1)}
+    ring_unsplit = {(1, 4, 4, 8, 4, 1), (2, 2, 4, 4, 4, 1), (1, 4, 4, 4, 2, 1), (2, 2, 4, 8, 8, 1), (2, 2, 4, 8, 6, 1)}
     for _ in range(400):
         m = int(rng.integers(1, 20000))
         n = int(rng.integers(1, 4000)) * 8
@@ -451,15 +452,16 @@ def test_widen_first_only_on_ring_tiles_with_a_measured_lead():
 
 
 def test_wide_tile_rule():
-    """The wide tile's regime (fp16 activations): shapes on its grid with K >= 3072 whose last round of 256 tiles is
-    whole or at least 170 / 256 full, or at least 1700 tiles; a single partial round only from K = 4096. One cell
-    each way from the tile sweep."""
+    """The 256 x 256 wide tile's regime (fp16 activations): shapes on its grid with K >= 3072 whose last round of
+    256 tiles is whole or at least 170 / 256 full, or at least 1700 tiles; a single partial round only from
+    K = 4096; not where the 256 x 192 tile makes one round 205 / 256 full or more. One cell each way from the
+    tile sweep."""
     from feather_ops.scaled_mm import select_scaled_mm_config as pick
 
     wide = (2, 2, 4, 8, 8, 1)
     assert pick(4096, 4096, 4096) == wide               # one whole round: 1.067 over the ring
     assert pick(5376, 5376, 7168) == wide               # 441 tiles, last round 185 / 256: 1.044
-    assert pick(9216, 1280, 5120) == wide               # one round of 180: 1.073
+    assert pick(4096, 3328, 4096) == wide               # one round of 208 (the 256 x 192 tile: 288)
     assert pick(9216, 18432, 3072) == wide              # 2592 tiles: 1.019
     assert pick(4096, 3072, 3072) != wide               # one partial round at K = 3072: 0.988
     assert pick(4096, 4608, 4608) != wide               # 288 tiles: a 32-tile second round, 0.78
@@ -467,6 +469,26 @@ def test_wide_tile_rule():
     assert pick(4096, 8192, 2048) != wide               # K < 3072
     assert pick(4112, 4096, 4096) != wide               # off the grid: masked loads
     assert pick(4096, 12288, 3072, torch.bfloat16) != wide   # bf16 in place: the ring tiles
+
+
+def test_wide192_tile_rule():
+    """The 256 x 192 wide tile's regime (fp16 activations): one round of its tiles at least 205 / 256 full, K >= 3072
+    and a multiple of 64, any M and N. The cells of the tile sweep it wins, and its losses either side."""
+    from feather_ops.scaled_mm import select_scaled_mm_config as pick
+
+    w192 = (2, 2, 4, 8, 6, 1)
+    assert pick(4096, 3072, 3072) == w192               # C2: 256 tiles, 1.114 over the best other tile
+    assert pick(4096, 3072, 12288) == w192              # 1.097
+    assert pick(6416, 1536, 6144) == w192               # 26 x 8 = 208 tiles (ragged M): 1.052
+    assert pick(9232, 1024, 5120) == w192               # 37 x 6 = 222 (ragged M and N): 1.051
+    assert pick(9216, 1280, 5120) == w192               # 252: 1.023
+    assert pick(4112, 2560, 6912) == w192               # 238: 1.022
+    assert pick(4112, 3072, 3072) != w192               # 272 tiles, a second round: 0.60
+    assert pick(4096, 4608, 4608) != w192               # 384: 0.97
+    assert pick(4096, 4096, 4096) != w192               # 352: 0.66
+    assert pick(1024, 10240, 1280) != w192              # 216 tiles, K < 3072: 0.96
+    assert pick(6144, 1536, 4112) != w192               # K not a multiple of 64
+    assert pick(4096, 3072, 3072, torch.bfloat16) != w192   # bf16 in place: the ring tiles
 
 
 def test_heuristic_returns_instantiated_tiles():
@@ -486,7 +508,7 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(4096, 12288, 3072) == (2, 2, 4, 8, 8, 1)   # C3: 3 full rounds of the wide tile
     assert pick(4112, 12288, 3072) == (1, 4, 4, 8, 4, 1)   # ragged M: 128 x 256 as 128 x 64 waves
     assert pick(4096, 12288, 3072, torch.bfloat16) == (2, 2, 4, 4, 8, 1)   # bf16: 64 x 128 waves
-    assert pick(4096, 3072, 3072) == (2, 2, 4, 4, 4, 1)    # C2: one full wave of 128 x 128
+    assert pick(4096, 3072, 3072) == (2, 2, 4, 8, 6, 1)    # C2: one full round of 256 x 192
     assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
     assert pick(4112, 1024, 5120) == (1, 4, 4, 4, 2, 1)    # one partial wave: 64 x 128 ring tiles
     assert pick(2304, 1280, 1280) == (2, 2, 4, 2, 2, 1)    # small grid, short K: 64 x 64 ring
