@@ -1264,16 +1264,19 @@ __global__ __launch_bounds__(kWave * KS * WN) void stream_kernel(const Params p)
             const int col = tn * S::kBN + cb;
             // N % 8 == 0, so a piece lies wholly inside N or wholly outside
             const bool ok = row < p.M && col < p.N;
-            const u32x4 bias_bits = has_bias ? buf_load16(bias_rsrc, ok ? static_cast<uint32_t>(col) * 2u : kOob)
-                                             : u32x4{0u, 0u, 0u, 0u};
+            // two 8-byte loads: the bias is only 8-byte aligned (the C ABI's contract)
+            const u32x2 bias_lo = has_bias ? buf_load8(bias_rsrc, ok ? static_cast<uint32_t>(col) * 2u : kOob)
+                                           : u32x2{0u, 0u};
+            const u32x2 bias_hi = has_bias ? buf_load8(bias_rsrc, ok ? static_cast<uint32_t>(col + 4) * 2u : kOob)
+                                           : u32x2{0u, 0u};
             f32x4 sc_lo = f32x4{scale, scale, scale, scale};
             f32x4 sc_hi = sc_lo;
             if (p.col_scale) {
                 sc_lo = __builtin_bit_cast(f32x4, buf_load16(scale_rsrc, ok ? static_cast<uint32_t>(col) * 4u : kOob));
                 sc_hi = __builtin_bit_cast(f32x4, buf_load16(scale_rsrc, ok ? static_cast<uint32_t>(col + 4) * 4u : kOob));
             }
-            const u32x2 y_lo = epilogue4<kOutBf16>(lo, sc_lo, has_bias, u32x2{bias_bits[0], bias_bits[1]});
-            const u32x2 y_hi = epilogue4<kOutBf16>(hi, sc_hi, has_bias, u32x2{bias_bits[2], bias_bits[3]});
+            const u32x2 y_lo = epilogue4<kOutBf16>(lo, sc_lo, has_bias, bias_lo);
+            const u32x2 y_hi = epilogue4<kOutBf16>(hi, sc_hi, has_bias, bias_hi);
             const uint32_t off = ok ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(p.N) +
                                        static_cast<uint32_t>(col)) * 2u
                                     : kOob;

@@ -650,3 +650,28 @@ def test_split_k_at_the_maximum_split_count(fo):
     bias = _tensor((N,), torch.bfloat16, seed=2)
     out = fo.scaled_mm_hip(a, bp, None, bias, torch.bfloat16, tile=(2, 2, 4, 4, 4, 1), splits=32)
     check_against_oracle(out, a, bp, None, bias)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tile,m", [
+    ((4, 1, 4, 1, 4, 0), 16),     # streaming, 64 columns: the row-piece join
+    ((2, 2, 4, 4, 2, 0), 64),     # streaming, 64 rows: the row-piece join
+    ((8, 1, 4, 1, 1, 0), 16),     # streaming, 16 columns: the per-fragment join
+    ((1, 4, 4, 8, 4, 1), 300),    # ring
+    ((2, 2, 4, 8, 8, 1), 300),    # wide 256 x 256
+    ((2, 2, 4, 8, 6, 1), 300),    # wide 256 x 192
+])
+def test_bias_at_an_8_byte_offset(fo, tile, m, out_dtype):
+    """The contract asks only 8-byte alignment of the bias: a bias view starting 8 bytes into its buffer (not 16-byte
+    aligned) gives the same bits as an aligned copy, on every epilogue form."""
+    n, k = 776, 512
+    a = _tensor((m, k), torch.float16, seed=3)
+    bp = fo.prepack_b_for_scaled_mm(_tensor((k, n), torch.float8_e5m2, seed=4))
+    s = torch.tensor(0.5, device="cuda")
+    buf = _tensor((n + 4,), out_dtype, seed=5)
+    bias = buf[4:]
+    assert bias.data_ptr() % 16 == 8
+    shifted = fo.scaled_mm_hip(a, bp, s, bias, out_dtype, tile=tile)
+    aligned = fo.scaled_mm_hip(a, bp, s, bias.clone(), out_dtype, tile=tile)
+    assert torch.equal(shifted.view(torch.int16), aligned.view(torch.int16))
+    check_against_oracle(aligned, a, bp, s, bias.clone())
