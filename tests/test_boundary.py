@@ -314,7 +314,7 @@ def test_heuristic_splits_k_on_underfilled_grids_with_long_k():
     assert auto(1536, 1024, 1536) == ((2, 2, 4, 2, 2, 1), 1)    # 384 tiles, 24 stages: unsplit
     assert auto(1024, 1280, 1280) == ((4, 1, 4, 1, 4, 0), 1)    # 320 tiles fill 5/8: streaming
     assert auto(768, 1024, 2048) == ((4, 1, 4, 1, 4, 0), 1)     # M <= 768: streaming
-    assert auto(192, 1536, 6144) == ((4, 1, 4, 1, 4, 0), 1)     # 24 tiles: too few to split into
+    assert auto(192, 1536, 6144) == ((2, 2, 4, 2, 2, 0), 1)     # too few tiles to split: the 32-row tile's round
     # 64 < M <= 192: streaming below a 24 MiB weight, the split 64 x 128 ring tile from there on
     assert auto(192, 4096, 4096) == ((4, 1, 4, 1, 4, 0), 1)     # 16 MiB, 64 tiles of 128 x 128
     assert auto(128, 4096, 14336) == ((1, 4, 4, 4, 2, 1), 8)    # 56 MiB, 32 tiles: 64 tiles x 8 = 512
@@ -489,6 +489,25 @@ def test_wide192_tile_rule():
     assert pick(1024, 10240, 1280) != w192              # 216 tiles, K < 3072: 0.96
     assert pick(6144, 1536, 4112) != w192               # K not a multiple of 64
     assert pick(4096, 3072, 3072, torch.bfloat16) != w192   # bf16 in place: the ring tiles
+
+
+def test_stream32_tile_rule_for_m_over_64():
+    """64 < M <= 256 on the streaming tiles with fp16 activations: the 32-row tile when it makes one round of 144-256 blocks
+    (it reads the weight half as often as the 16-row tiles); never with bf16 activations, which it widens per
+    fragment. Cells of the fitting sweep and of the held-out one."""
+    from feather_ops.scaled_mm import select_scaled_mm_config as pick
+
+    s32, s16 = (2, 2, 4, 2, 2, 0), (4, 1, 4, 1, 4, 0)
+    assert pick(128, 4096, 4096) == s32        # 256 blocks: 1.116 over the 16-row tile
+    assert pick(192, 2560, 2560) == s32        # 240: 1.148
+    assert pick(96, 3072, 3072) == s32         # 144: 1.010
+    assert pick(256, 1536, 6144) == s32        # 192 (held out): 1.212
+    assert pick(80, 5120, 1280) == s32         # 240 (held out): 1.025
+    assert pick(96, 2560, 2560) == s16         # 120 blocks: 0.828
+    assert pick(192, 4096, 4096) == s16        # 384 blocks, a second round: 0.943
+    assert pick(64, 4096, 4096) == s16         # M = 64: the 16-row tile (0.777)
+    assert pick(128, 4096, 4096, torch.bfloat16) == s16   # bf16 activations: 0.82 on the held-out cells
+    assert pick(512, 1024, 1024) == s16        # past the rows the sweeps covered
 
 
 def test_heuristic_returns_instantiated_tiles():
