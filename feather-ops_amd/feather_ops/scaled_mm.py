@@ -51,6 +51,7 @@ _STREAM_32_MAX_M = 256   # the rows its sweeps covered
 # wave (16 KiB of weight per wave at 64 columns), 4 slices keep ~32 KiB per CU in flight where 8 keep ~64 KiB,
 # which oversubscribes HBM on weights of 50-100 MB (C4: 11.86 against 12.14 us, graph-timed, cold weights).
 _TILE_STREAM_16x64_KS4 = (4, 1, 4, 1, 4, 0)
+_TILE_STREAM_16x64_U8 = (4, 1, 8, 1, 4, 0)
 _TILE_STREAM_16x32 = (8, 1, 4, 1, 2, 0)
 
 # MI355X: 256 compute units.
@@ -184,6 +185,26 @@ _STREAM_SPLIT_COUNTS = (8, 6, 4, 3, 2)
 _STREAM_SPLIT_MIN_RANGE = 3072
 _STREAM_SPLIT_MIN_WORKGROUPS = 128
 _STREAM_SPLIT_CAP_PER_ROW = 64
+# M > 64 (five or more rows of 16-row tiles), measured on a 96-cell grid (M 80-256, N 1024-3072, K 6144-16384,
+# fp16 and bf16, graph replays, cold weights):
+# - the long-K split keeps within one workgroup per CU (the per-row allowance above let 160-tile grids split
+#   into 320 workgroups: 0.83-0.85x the unsplit tile);
+# - one round of unsplit 16 x 64 blocks with K >= 6144 takes the tile with more weight in flight, the weight's
+#   re-reads then coming from the caches: 128-deep steps (fp16 1.03-1.11x over the 4-slice 64-deep tile on every
+#   such cell; bf16 from K = 12288) or 8 K slices (bf16 below K = 12288, 1.04-1.12x);
+# - the ring tiles' split-K needs enough tiles: with fewer than 36 64 x 128 tiles it lost on every cell
+#   (0.50-0.94x at 16-32 tiles, where 8 splits still leave CUs idle and each split is short); with 36-79 it won
+#   only on weights of 18 MiB and more (N x K 1536 x 12288 on: 0.99-1.0 of the best; 12.6-16.8 MB 0.83-0.88),
+#   and with bf16 activations (widened in registers on that ring) only from 64 tiles (0.70-0.84x at 36-48);
+# - the 32-row streaming tile's one-round rule (`_STREAM_32_MIN_BLOCKS`) holds at K >= 6144 only from M = 160
+#   (at M 80-128 the deeper 16-row tiles are 1.1-1.3x faster there).
+_STREAM_DEEP_MIN_K = 6144
+_STREAM_DEEP_KS8_MAX_K_BF16 = 12288
+_RING_SPLIT_MIN_TILES = 80
+_RING_SPLIT_FEW_TILES = 36
+_RING_SPLIT_FEW_TILES_BF16 = 64
+_RING_SPLIT_FEW_TILES_MIN_WEIGHT = 18 << 20
+_STREAM_32_LONG_K_MIN_M = 160
 # Except: M <= _STREAM_UNSPLIT_TINY_M on a weight whose 16-column fragments fill one round of 192-256 blocks
 # (N 3072-4096) and K up to _STREAM_UNSPLIT_MAX_K runs unsplit on the 16 x 16 tile, which keeps three fetches
 # in flight per wave: 1.02-1.2x over the 16 x 32 tile split 2 ways on 21 of 24 cells (M 1-4, K 8192-16384;
@@ -239,7 +260,7 @@ def _stream_split(M: int, N: int, K: int) -> tuple[tuple[int, int, int, int, int
     tiles = _blocks(M, N, tile)
     # more row tiles share each weight panel (its second read hits the caches), and tolerate a few more
     # workgroups than CUs: 32 x 5120 x 13824 runs 1.27x faster split 2 ways (320 workgroups) than unsplit
-    cap = _CUS + _STREAM_SPLIT_CAP_PER_ROW * (-(-M // 16) - 1)
+    cap = _CUS if M > 64 else _CUS + _STREAM_SPLIT_CAP_PER_ROW * (-(-M // 16) - 1)
     for splits in _STREAM_SPLIT_COUNTS:
         if tiles * splits <= cap and K // splits >= _STREAM_SPLIT_MIN_RANGE:
             if tiles * splits > _STREAM_SPLIT_MIN_WORKGROUPS or tiles * splits > _stream_unsplit_shape(M, N)[1]:
@@ -341,7 +362,9 @@ def select_scaled_mm_config(
       fp16 activations, as 2 x 2 waves of 64 x 128 with bf16 ones.
     - M > 64 with a smaller grid and K >= 4096, once the 16-row streaming tile would read 216 MiB of
       weight or more (N * K bytes once per 16 rows, over the fraction of CU slots its blocks fill in their
-      last round): the 64 x 128 ring tile (deep ring) up to 256 of its tiles, split along K
+      last round), given at least 80 64 x 128 tiles, or 36 (bf16 activations: 64) on a weight of 18 MiB or
+      more (with fewer, the split ring lost to the streaming tiles on every cell of a 96-cell grid, 0.50-0.94x):
+      the 64 x 128 ring tile (deep ring) up to 256 of its tiles, split along K
       (`select_scaled_mm_splits`); beyond that the 64 x 128 or 128 x 128 ring tile and split count with the
       least modelled time (`_small_grid_choice`: 0.990 of the best candidate in geometric mean on 58 fp16
       cells of that regime, 0.994 on 30 held-out ones and 0.994 / 0.983 with bf16 activations, against
@@ -372,10 +395,16 @@ def select_scaled_mm_config(
       0.83-0.94x; on 18 held-out cells, M 80-256, 1.01-1.21x on 16 and 0.989-0.998x on 2). Not with bf16
       activations (0.72-0.92x on the same 18 cells).
     - K >= 8192 with at most 170 16 x 64 streaming tiles: the 16 x 32 tile (8 K slices) for M <= 12, the
-      16 x 64 tile (4 K slices) above, split along K to at most one workgroup per CU
-      (`select_scaled_mm_splits`), where that gives more workgroups than the unsplit rule below.
+      16 x 64 tile (4 K slices) above, split along K to at most one workgroup per CU (for M <= 64 plus 64 per
+      further row of tiles) (`select_scaled_mm_splits`), where that gives more workgroups than the unsplit
+      rule below.
     - Otherwise the 16-row split-K streaming tile, as wide as still gives 160 blocks (64, 32 or 16
-      columns): 16 x 64 with 4 K slices, the narrower ones with 8 up to one block per CU and 4 beyond.
+      columns): 16 x 64 with 4 K slices, the narrower ones with 8 up to one block per CU and 4 beyond; for
+      M > 64 and K >= 6144, one round of 16 x 64 blocks keeps more weight in flight: 128-deep steps with fp16
+      activations (1.03-1.11x), 8 K slices with bf16 ones below K = 12288 and 128-deep steps from it
+      (1.04-1.12x). Over the 96-cell grid these M > 64 rules took the picks from 0.923 to 0.988 of the best
+      candidate (bf16 0.915 to 0.975), and on 60 held-out cells (M 72-240, N 1280-3584, K 5120-14336) from
+      0.952 to 0.968 (bf16 0.927 to 0.966).
     The streaming picks were refitted after the streaming kernel's loop kept two fetches in flight per wave
     (it had been one): on 193 swept cells with M <= 256 the picks are at 0.994 of the best candidate in
     geometric mean, against 0.953 for the rules before.
@@ -390,7 +419,11 @@ def select_scaled_mm_config(
             return _TILE_WIDE
         return min(_RING_MODEL if a_bf16 else _RING_MODEL_FP16, key=lambda entry: _ring_time(M, N, *entry))[0]
     min_reread = _BF16_RING_MIN_REREAD if a_bf16 else _RING_MIN_REREAD
-    ring_split = M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
+    ring_tiles = _blocks(M, N, _TILE_RING_64x128)
+    few_tiles = _RING_SPLIT_FEW_TILES_BF16 if a_bf16 else _RING_SPLIT_FEW_TILES
+    ring_split = (M > 64 and K >= _SPLIT_MIN_K and _stream_reread(M, N, K) >= min_reread
+                  and (ring_tiles >= _RING_SPLIT_MIN_TILES
+                       or (ring_tiles >= few_tiles and N * K >= _RING_SPLIT_FEW_TILES_MIN_WEIGHT)))
     if ring_split and _blocks(M, N, _TILE_RING_64x128) <= _CUS:
         return _TILE_RING_64x128
     if ring_split:
@@ -413,9 +446,12 @@ def select_scaled_mm_config(
             return split[0]
     if M > 768 and not a_bf16 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
         return _TILE_RING_64x64
-    if 64 < M <= _STREAM_32_MAX_M and not a_bf16 and _STREAM_32_MIN_BLOCKS <= blocks_32 <= _CUS:
+    if (64 < M <= _STREAM_32_MAX_M and not a_bf16 and _STREAM_32_MIN_BLOCKS <= blocks_32 <= _CUS
+            and (K < _STREAM_DEEP_MIN_K or M >= _STREAM_32_LONG_K_MIN_M)):
         return _TILE_STREAM_32x64
     repeat_n, blocks = _stream_unsplit_shape(M, N)
+    if M > 64 and repeat_n == 4 and blocks <= _CUS and K >= _STREAM_DEEP_MIN_K:
+        return _TILE_STREAM_16x64 if a_bf16 and K < _STREAM_DEEP_KS8_MAX_K_BF16 else _TILE_STREAM_16x64_U8
     # 8 K slices while the blocks fit one per CU, 4 beyond; the 64-column tile takes 4 either way (its 8-slice
     # form keeps twice the weight in flight, past what the HBM serves best: C4 2.5% slower with it)
     return (8 if blocks <= _CUS and repeat_n < 4 else 4, 1, 4, 1, repeat_n, 0)

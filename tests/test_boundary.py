@@ -510,6 +510,29 @@ def test_stream32_tile_rule_for_m_over_64():
     assert pick(512, 1024, 1024) == s16        # past the rows the sweeps covered
 
 
+def test_mid_m_streaming_and_ring_split_rules():
+    """M > 64 with a small grid (96-cell fitting grid, M 80-256, N 1024-3072, K 6144-16384, and a 60-cell held-out
+    one): long-K streaming splits stay within one workgroup per CU; one round of unsplit 16 x 64 blocks at K >= 6144
+    keeps more weight in flight (fp16: 128-deep steps; bf16: 8 K slices, 128-deep steps from K = 12288); the ring
+    tiles' split needs 80 64 x 128 tiles, or 36 (bf16: 64) on a weight of 18 MiB or more. Each cell below is the
+    best or within 3% of the best measured candidate; the comment gives the previous pick's ratio."""
+    from feather_ops.scaled_mm import _auto_choice
+
+    fp, bf = torch.float16, torch.bfloat16
+    u8, ks8, ks4 = (4, 1, 8, 1, 4, 0), (8, 1, 4, 1, 4, 0), (4, 1, 4, 1, 4, 0)
+    ring, s32 = (1, 4, 4, 4, 2, 1), (2, 2, 4, 2, 2, 0)
+    assert _auto_choice(160, 1024, 8192, fp) == (u8, 1, False)      # split 2 into 320 workgroups: 0.83
+    assert _auto_choice(128, 2048, 8192, fp) == (u8, 1, False)      # 4 K slices: 0.90
+    assert _auto_choice(128, 2048, 8192, bf) == (ks8, 1, False)     # 0.90
+    assert _auto_choice(128, 2048, 12288, bf) == (u8, 1, False)     # 0.91
+    assert _auto_choice(80, 1024, 16384, fp) == (ks4, 3, False)     # the ring split on 16 tiles: 0.50
+    assert _auto_choice(96, 3072, 12288, bf) == (ks4, 1, False)     # the ring split on 48 tiles (bf16): 0.70
+    assert _auto_choice(192, 1536, 8192, fp) == (s32, 1, False)     # the ring split on a 12.6 MB weight: 0.88
+    assert _auto_choice(192, 1536, 12288, fp) == (ring, 7, False)   # 36 tiles, 18.9 MB: the ring split stays
+    assert _auto_choice(256, 3072, 12288, bf) == (ring, 8, False)   # 96 tiles: the ring split stays
+    assert _auto_choice(96, 3072, 6144, fp) == (ks4, 1, False)      # K >= 6144, M < 160: not the 32-row tile
+
+
 def test_heuristic_returns_instantiated_tiles():
     from feather_ops.scaled_mm import select_scaled_mm_config
     from feather_ops.tiles import SCALED_MM_TILES
