@@ -492,7 +492,7 @@ def test_wide192_tile_rule():
 
 
 def test_stream32_tile_rule_for_m_over_64():
-    """64 < M <= 256 on the streaming tiles with fp16 activations: the 32-row tile when it makes one round of 144-256 blocks
+    """64 < M <= 512 on the streaming tiles with fp16 activations: the 32-row tile when it makes one round of 144-256 blocks
     (it reads the weight half as often as the 16-row tiles); never with bf16 activations, which it widens per
     fragment. Cells of the fitting sweep and of the held-out one."""
     from feather_ops.scaled_mm import select_scaled_mm_config as pick
@@ -507,7 +507,10 @@ def test_stream32_tile_rule_for_m_over_64():
     assert pick(192, 4096, 4096) == s16        # 384 blocks, a second round: 0.943
     assert pick(64, 4096, 4096) == s16         # M = 64: the 16-row tile (0.777)
     assert pick(128, 4096, 4096, torch.bfloat16) == s16   # bf16 activations: 0.82 on the held-out cells
-    assert pick(512, 1024, 1024) == s16        # past the rows the sweeps covered
+    assert pick(512, 1024, 1024) == s32        # 256 blocks: 1.16
+    assert pick(384, 1280, 4096) == s32        # 240: 1.21
+    assert pick(512, 1152, 1152) == s16        # 288 blocks, a second round: 0.91
+    assert pick(1024, 1024, 1024) != s32       # past the rows the sweeps covered
 
 
 def test_mid_m_streaming_and_ring_split_rules():
@@ -554,7 +557,7 @@ def test_heuristic_picks_on_representative_cells():
     assert pick(9216, 2048, 2048) == (2, 2, 4, 4, 4, 1)    # 128 x 256 would need a second, 1/8-full wave
     assert pick(4112, 1024, 5120) == (1, 4, 4, 4, 2, 1)    # one partial wave: 64 x 128 ring tiles
     assert pick(2304, 1280, 1280) == (2, 2, 4, 2, 2, 1)    # small grid, short K: 64 x 64 ring
-    assert pick(512, 1024, 1024) == (4, 1, 4, 1, 4, 0)     # tiny grid: streaming, 4 K slices
+    assert pick(512, 1024, 1024) == (2, 2, 4, 2, 2, 0)     # tiny grid: one round of 32-row streaming blocks
     assert pick(32, 25600, 2048) == (2, 2, 4, 2, 2, 0)     # 32 rows, wide: 32-row streaming tile
     assert pick(32, 25600, 5120) == (1, 4, 4, 4, 2, 1)     # ... and a 131 MB weight: the 64 x 128 ring tile
     assert pick(32, 11264, 11264) == (2, 2, 4, 2, 2, 1)    # 127 MB, 176 64 x 64 tiles: that ring tile
