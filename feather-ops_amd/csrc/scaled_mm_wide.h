@@ -110,7 +110,10 @@ __device__ __forceinline__ uint32_t decode_word(uint32_t w, bool hi) {
 // fragment row's goes in the scalar offset and a pair's in the instruction's. kRagged: rows past M and columns
 // past N (N % 8 == 0, so a piece of 8 columns is wholly in or out) take an out-of-range offset, dropped by the
 // buffer's range check. Scheduling barriers keep the pairs in order, so that only one pair's values are held in
-// VGPRs at a time.
+// VGPRs at a time. The stores write through at device scope: the output's lines leave L2 as they are written
+// instead of staying dirty there until the end of the launch (measured on copies of the kernel, interleaved
+// runs: C3 0.5% faster, C2's shape, one round of 256 x 192 tiles, 2.6%; the non-temporal hint instead, 2%
+// slower).
 template <int RM, int RN, bool kOutBf16, bool kBias, bool kColScale, bool kRagged>
 __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32x4 (&acc)[RM][RN], int row0, int col0,
                                                       int lane, float scale) {
@@ -148,10 +151,11 @@ __device__ __forceinline__ void store_wave_tiles_swap(const Params& p, const f32
             if constexpr (kRagged) {
                 const bool ok = row0 + 16 * i + r16 < p.M && col + 32 * jp < p.N;
                 const uint32_t off = ok ? base + static_cast<uint32_t>(16 * i) * pitch + 64u * jp : kOob;
-                __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(off), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(off), 0, kDeviceScope);
             } else {
                 __builtin_amdgcn_raw_buffer_store_b128(v, c_rsrc, static_cast<int>(base + 64u * jp),
-                                                       static_cast<int>(static_cast<uint32_t>(16 * i) * pitch), 0);
+                                                       static_cast<int>(static_cast<uint32_t>(16 * i) * pitch),
+                                                       kDeviceScope);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
