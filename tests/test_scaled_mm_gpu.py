@@ -219,7 +219,12 @@ HEURISTIC_CELLS = [
     (2304, 1280, 1280),  # 64 x 64 ring tile
     (1000, 1000, 2560),  # 64 x 64 ring tile split 2 ways (M > 768, 256 tiles, ragged M and N)
     (4112, 1024, 5120),  # 64 x 128 ring tile, one partial wave
-    (512, 1024, 1024),   # 4-slice streaming tile
+    (512, 1024, 1024),   # 32-row streaming tile (fp16), 4-slice streaming tile (bf16)
+    (384, 1280, 4096),   # 32-row streaming tile past 256 rows (fp16)
+    (160, 1024, 8192),   # 16 x 64, 8 slices of unroll 1 (fp16) / 4 slices of unroll 2 (bf16): deep K
+    (128, 2048, 8192),   # the same deep-K streaming tiles at 128 rows
+    (80, 1024, 16384),   # 4-slice streaming tile split 3 ways (few ring tiles: not a ring split)
+    (4096, 3072, 3072),  # 256 x 192 wide tile, one round of 256 (bf16 activations: widened first)
     (9216, 2048, 2048),  # 128 x 128 (one full wave of blocks)
     (2320, 6144, 6144),  # 128 x 256 (bf16 activations: widened first, then 128 x 64 waves)
     (2048, 8192, 2048),  # 128 x 256 (bf16 activations: widened first, then 128 x 64 waves)
