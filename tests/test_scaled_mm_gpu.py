@@ -301,13 +301,13 @@ def test_bf16_widened_first_is_bit_identical(fo, m, n, k):
         assert torch.equal(auto.view(torch.int16), in_place.view(torch.int16))
 
 
-def _random_cases(count: int = 16, seed: int = 11):
+def _random_cases(count: int = 16, seed: int = 11, rows=(1, 7, 16, 40, 77, 300, 1000, 2048, 4097, 9000)):
     """Seeded shapes across the heuristic's regimes (M 1-9000, N and K multiples of 8 and 16 up to 14336), each
     with its activation dtype, weight format, output dtype, bias and scale form."""
     rng = np.random.default_rng(seed)
     cases = []
     while len(cases) < count:
-        m = int(rng.choice([1, 7, 16, 40, 77, 300, 1000, 2048, 4097, 9000]))
+        m = int(rng.choice(rows))
         n = int(rng.integers(1, 14336 // 8 + 1)) * 8
         k = int(rng.integers(1, 14336 // 16 + 1)) * 16
         if m * n * k > (1 << 37) or m * k > (1 << 25):
@@ -317,7 +317,9 @@ def _random_cases(count: int = 16, seed: int = 11):
     return cases
 
 
-@pytest.mark.parametrize("m,n,k,a_bf16,e5m2,out_bf16,has_bias,scale_mode", _random_cases())
+# the second batch: M 65-512, where the streaming tiles (32-row, deep-K, split) and the split ring tiles meet
+@pytest.mark.parametrize("m,n,k,a_bf16,e5m2,out_bf16,has_bias,scale_mode",
+                         _random_cases() + _random_cases(12, 23, (80, 96, 128, 160, 200, 256, 320, 384, 448, 512)))
 def test_random_shapes_auto_path(fo, m, n, k, a_bf16, e5m2, out_bf16, has_bias, scale_mode):
     """The whole auto path (tile, split count and, for bf16 activations, the widening pass) on seeded random
     shapes and argument forms, against the oracle on sampled rows."""
