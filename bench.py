@@ -72,57 +72,76 @@ def measured_traffic(cell: str, tile) -> float | None:
 
 
 class ClockMonitor:
-    """The GPU's shader clock while a load runs: a thread reads the SMU's metrics table (amdsmi
-    `gpu_metrics`: current GFX clock of every XCD) every `period_s` between start() and stop(). The table
-    is the power management's own view, refreshed every few milliseconds; a clock read between kernels
-    instead (a few microseconds after the MFMA load stops) already shows it recovering toward 2.4 GHz, so
-    the sampling has to run during the load. Unavailable (amdsmi missing, no matching device): samples
-    stay empty and summary() returns None."""
+    """The GPU's shader clock while a load runs, from the SMU's metrics table (amdsmi `gpu_metrics`: the
+    current GFX clock of every XCD). The SMU rewrites that table once a second (its `system_clock_counter`,
+    in ns, steps by 10^9 between rewrites), so a thread polls it every `period_s` and keeps each rewrite once;
+    the table present when start() is called was written before the load window and is dropped. A clock read
+    between kernels instead (a few microseconds after the MFMA load stops) already shows it recovering
+    toward 2.4 GHz, so the window must be loaded throughout. Unavailable (amdsmi missing, no matching
+    device): no rewrites are kept and summary() returns None. `reader` (tests) replaces amdsmi: it returns
+    (table counter, [per-XCD MHz])."""
 
-    def __init__(self, period_s: float = 0.002):
-        import threading
-
+    def __init__(self, period_s: float = 0.002, reader=None):
         self.period_s = period_s
-        self.samples = []
-        self._stop = threading.Event()
+        self.tables = []          # (perf_counter when first seen, table counter, [per-XCD MHz])
+        self._stale = None
+        self._stop = None
         self._thread = None
-        self._handle = None
-        self._amdsmi = None
-        try:
-            import amdsmi
+        self._read = reader
+        if reader is None:
+            try:
+                import amdsmi
 
-            amdsmi.amdsmi_init()
-            handles = amdsmi.amdsmi_get_processor_handles()
-            if len(handles) == 1:
-                self._handle = handles[0]
-                self._amdsmi = amdsmi
-        except Exception:  # amdsmi absent or refused: no clock figure, the benchmark itself is unaffected
-            self._amdsmi = None
+                amdsmi.amdsmi_init()
+                handles = amdsmi.amdsmi_get_processor_handles()
+                if len(handles) == 1:
+                    handle = handles[0]
 
-    def _read(self):
-        metrics = self._amdsmi.amdsmi_get_gpu_metrics_info(self._handle)
-        clks = [c for c in (metrics.get("current_gfxclks") or []) if isinstance(c, int) and 0 < c < 10000]
-        return clks
+                    def read():
+                        metrics = amdsmi.amdsmi_get_gpu_metrics_info(handle)
+                        clks = [c for c in (metrics.get("current_gfxclks") or [])
+                                if isinstance(c, int) and 0 < c < 10000]
+                        return metrics.get("system_clock_counter"), clks
 
-    def _run(self):
+                    self._read = read
+            except Exception:  # amdsmi absent or refused: no clock figure, the benchmark itself is unaffected
+                self._read = None
+
+    def _poll(self):
+        """Keep the table if it is a rewrite not seen yet; False once the reader fails."""
         import time as _time
 
+        try:
+            counter, clks = self._read()
+        except Exception:
+            return False
+        seen = self.tables[-1][1] if self.tables else self._stale
+        if clks and counter is not None and counter != seen:
+            self.tables.append((_time.perf_counter(), counter, clks))
+        return True
+
+    def _run(self):
         while not self._stop.is_set():
-            try:
-                clks = self._read()
-            except Exception:
+            if not self._poll():
                 return
-            if clks:
-                self.samples.append((_time.perf_counter(), clks))
             self._stop.wait(self.period_s)
 
     def start(self):
         import threading
 
-        if self._amdsmi is not None:
-            self._stop.clear()
-            self._thread = threading.Thread(target=self._run, daemon=True)
-            self._thread.start()
+        if self._read is None:
+            return
+        try:
+            self._stale = self._read()[0]
+        except Exception:
+            self._read = None
+            return
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+
+    def rewrites(self) -> int:
+        return len(self.tables)
 
     def stop(self):
         if self._thread is not None:
@@ -131,17 +150,18 @@ class ClockMonitor:
             self._thread = None
 
     def summary(self) -> dict | None:
-        """Median over the samples of the mean XCD clock, its p10/p90, and each XCD's median; None without samples."""
-        if not self.samples:
+        """Median over the window's table rewrites of the mean XCD clock, its range, and each XCD's median;
+        None without a rewrite."""
+        if not self.tables:
             return None
-        means = [sum(c) / len(c) for _, c in self.samples]
-        n_xcd = min(len(c) for _, c in self.samples)
-        per_xcd = [_percentile([c[i] for _, c in self.samples], 0.5) for i in range(n_xcd)]
-        return {"clock_mhz": round(_percentile(means, 0.5), 1), "p10_mhz": round(_percentile(means, 0.1), 1),
-                "p90_mhz": round(_percentile(means, 0.9), 1), "per_xcd_mhz": [round(v, 1) for v in per_xcd],
-                "samples": len(means),
-                "method": "amdsmi gpu_metrics current_gfxclks (every XCD), sampled every 2 ms by a thread during "
-                          "the timed rounds"}
+        means = [sum(c) / len(c) for _, _, c in self.tables]
+        n_xcd = min(len(c) for _, _, c in self.tables)
+        per_xcd = [_percentile([c[i] for _, _, c in self.tables], 0.5) for i in range(n_xcd)]
+        return {"clock_mhz": round(_percentile(means, 0.5), 1), "min_mhz": round(min(means), 1),
+                "max_mhz": round(max(means), 1), "per_xcd_mhz": [round(v, 1) for v in per_xcd],
+                "table_rewrites": len(means),
+                "method": "amdsmi gpu_metrics current_gfxclks (every XCD), each once-a-second rewrite of the SMU's "
+                          "table during the timed rounds and the same launches continued after them"}
 
 
 def algorithmic_bytes(m: int, k: int, n: int, bias: bool = False) -> int:
@@ -182,14 +202,17 @@ def _percentile(values, q):
 
 
 def steady_rounds(launch_round, launches: int, rounds: int, warmup: int, min_warm_s: float = 1.0,
-                  max_warm_s: float = 6.0, tol: float = 0.02, monitor: "ClockMonitor | None" = None) -> dict:
+                  max_warm_s: float = 6.0, tol: float = 0.02, monitor: "ClockMonitor | None" = None,
+                  min_rewrites: int = 3, max_clock_s: float = 5.0) -> dict:
     """Time `launch_round` (enqueues `launches` kernel launches on the current stream) at steady state.
 
     `warmup` untimed launches' worth of rounds first, then more rounds until the clocks settle (at least
     min_warm_s of continuous work and the last three round times within `tol` of each other; at most
     max_warm_s), then `rounds` timed rounds. Each round is bracketed by device synchronisation and timed
     with HIP events on the launching stream. Returns microseconds per launch: median, p20, p80, plus the
-    warm-up actually run. A `monitor` (ClockMonitor) samples the clock during the timed rounds only.
+    warm-up actually run. A `monitor` (ClockMonitor) samples the clock from the first timed round on; as its
+    table is rewritten once a second, the same rounds continue untimed after the timed ones until it has
+    `min_rewrites` rewrites (at most `max_clock_s` of monitoring in all).
     """
     import torch
 
@@ -216,8 +239,11 @@ def steady_rounds(launch_round, launches: int, rounds: int, warmup: int, min_war
     warm_s = time.perf_counter() - t0
     if monitor is not None:
         monitor.start()
+    t_mon = time.perf_counter()
     timed = [one() for _ in range(rounds)]
     if monitor is not None:
+        while monitor.rewrites() < min_rewrites and time.perf_counter() - t_mon < max_clock_s:
+            one()
         monitor.stop()
     return {"us": _percentile(timed, 0.5), "p20_us": _percentile(timed, 0.2), "p80_us": _percentile(timed, 0.8),
             "rounds": rounds, "launches_per_round": launches, "warmup_launches": len(warm) * launches,

@@ -1,5 +1,5 @@
 """The tile-sweep harness (feather-ops_amd/benchmarks): grid integrity and the timing protocol's pure parts,
-on the CPU."""
+and bench.py's clock monitor, on the CPU."""
 
 import pytest
 
@@ -56,3 +56,33 @@ def test_weight_copies_exceed_the_mall_when_cold():
     assert weight_copies(12288, 3072, cold=False) == 1
     assert weight_copies(14336, 4096, cold=True) * 14336 * 4096 > 256e6
     assert weight_copies(248320, 4096, cold=True) == 1
+
+
+def test_clock_monitor_keeps_each_table_rewrite_once_and_drops_the_stale_one():
+    """The SMU table is rewritten once a second and polled every few ms: each rewrite counts once, and the
+    table present at start() (written before the load window) not at all."""
+    import bench
+
+    tables = iter([(100, [1400, 1500]), (100, [1400, 1500]), (100, [1400, 1500]),   # start() + stale polls
+                   (200, [2000, 1980]), (200, [2000, 1980]),
+                   (300, [1990, 1950]),
+                   (400, [2010, 2030]), (400, [2010, 2030])])
+    mon = bench.ClockMonitor(reader=lambda: next(tables))
+    mon._stale = mon._read()[0]
+    while mon._poll():
+        pass
+    assert [counter for _, counter, _ in mon.tables] == [200, 300, 400]
+    s = mon.summary()
+    assert s["table_rewrites"] == 3
+    assert s["clock_mhz"] == 1990.0 and s["min_mhz"] == 1970.0 and s["max_mhz"] == 2020.0
+    assert s["per_xcd_mhz"] == [2000.0, 1980.0]
+
+
+def test_clock_monitor_without_a_rewrite_reports_nothing():
+    import bench
+
+    mon = bench.ClockMonitor(reader=lambda: (7, [2000]))
+    mon._stale = mon._read()[0]
+    for _ in range(5):
+        assert mon._poll()
+    assert mon.summary() is None
