@@ -390,7 +390,7 @@ def select_scaled_mm_config(
       1.03-1.28x over two rows of the 16 x 64 tile on 24 cells, M 20-32, N 12288-16384, K 4096-5120, with
       three fetches in flight; at 288 blocks the small second round loses 6%).
     - 64 < M <= 512 where the rules above leave a streaming tile, fp16 activations: the 32-row streaming tile when it
-      gives one round of 144-256 blocks, which reads the weight half as often as the 16-row tiles (M 96-192, N x K
+      gives one round of 144-256 blocks (at K >= 6144 only from M = 160), which reads the weight half as often as the 16-row tiles (M 96-192, N x K
       2560^2-4096^2: 1.01-1.15x on the 6 such cells of a 48-cell sweep, each of the 3 outside that range
       0.83-0.94x; on 18 held-out cells, M 80-256, 1.01-1.21x on 16 and 0.989-0.998x on 2; at M 320-512 the best
       candidate on all 36 cells of a sweep, 1.03-1.26x). Not with bf16 activations (0.72-0.92x on the 18 cells).
