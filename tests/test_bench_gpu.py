@@ -1,0 +1,24 @@
+"""bench.py's headline measurement on the GPU: the C3 timing path and its clock figure."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def test_c3_timing_reports_the_clock_from_table_rewrites_under_load():
+    """The SMU table behind `clock_mhz` is rewritten once a second: the C3 timing keeps the load running until
+    the monitor has seen fresh rewrites, and the figure it reports lies in the range the GPU can run at."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import bench
+
+    if bench.ClockMonitor()._read is None:
+        pytest.skip("amdsmi unavailable: bench.py reports no clock")
+    c3 = bench.time_c3(steps=50, warmup=10, rounds=3)
+    clock = c3["clock"]
+    assert clock is not None
+    assert clock["table_rewrites"] >= 3
+    assert 500 <= clock["min_mhz"] <= clock["clock_mhz"] <= clock["max_mhz"] <= 2500
+    assert len(clock["per_xcd_mhz"]) == 8
+    assert 0 < c3["t"]["us"] < 1000
