@@ -47,6 +47,10 @@ _TILE_STREAM_16x64 = (8, 1, 4, 1, 4, 0)
 # even). With bf16 activations, which it widens per fragment, it is 0.72-0.92x the 16-row tile there.
 _STREAM_32_MIN_BLOCKS = 144
 _STREAM_32_MAX_M = 512   # the rows its sweeps covered
+# ... and for two rounds of 392-512 blocks: 0.998-1.149x the 16-row tile on the 7 such cells of three sweeps
+# (M 160-512, N x K 2048 x 1024 to 3584^2; about 1.08x in geometric mean), where 288-360 blocks lose (0.79-0.97x
+# on 11 cells: the second round's few blocks)
+_STREAM_32_TWO_ROUND_MIN_BLOCKS = 392
 # The same 16 x 64 block with 4 K slices (4 waves), and a 16 x 32 block with 8: with two fetches in flight per
 # wave (16 KiB of weight per wave at 64 columns), 4 slices keep ~32 KiB per CU in flight where 8 keep ~64 KiB,
 # which oversubscribes HBM on weights of 50-100 MB (C4: 11.86 against 12.14 us, graph-timed, cold weights).
@@ -390,10 +394,11 @@ def select_scaled_mm_config(
       1.03-1.28x over two rows of the 16 x 64 tile on 24 cells, M 20-32, N 12288-16384, K 4096-5120, with
       three fetches in flight; at 288 blocks the small second round loses 6%).
     - 64 < M <= 512 where the rules above leave a streaming tile, fp16 activations: the 32-row streaming tile when it
-      gives one round of 144-256 blocks (at K >= 6144 only from M = 160), which reads the weight half as often as the 16-row tiles (M 96-192, N x K
+      gives one round of 144-256 blocks or two of 392-512 (at K >= 6144 only from M = 160), which reads the weight half as often as the 16-row tiles (M 96-192, N x K
       2560^2-4096^2: 1.01-1.15x on the 6 such cells of a 48-cell sweep, each of the 3 outside that range
       0.83-0.94x; on 18 held-out cells, M 80-256, 1.01-1.21x on 16 and 0.989-0.998x on 2; at M 320-512 the best
-      candidate on all 36 cells of a sweep, 1.03-1.26x). Not with bf16 activations (0.72-0.92x on the 18 cells).
+      candidate on all 36 cells of a sweep, 1.03-1.26x; two rounds of 392-512 blocks 0.998-1.149x on 7 cells, where
+      288-360 blocks lose). Not with bf16 activations (0.72-0.92x on the 18 cells).
     - K >= 8192 with at most 170 16 x 64 streaming tiles: the 16 x 32 tile (8 K slices) for M <= 12, the
       16 x 64 tile (4 K slices) above, split along K to at most one workgroup per CU (for M <= 64 plus 64 per
       further row of tiles) (`select_scaled_mm_splits`), where that gives more workgroups than the unsplit
@@ -446,7 +451,8 @@ def select_scaled_mm_config(
             return split[0]
     if M > 768 and not a_bf16 and _ring_splits(M, N, K, _TILE_RING_64x64)[1] >= _BIG_M_RING_MIN_BUSY:
         return _TILE_RING_64x64
-    if (64 < M <= _STREAM_32_MAX_M and not a_bf16 and _STREAM_32_MIN_BLOCKS <= blocks_32 <= _CUS
+    if (64 < M <= _STREAM_32_MAX_M and not a_bf16
+            and (_STREAM_32_MIN_BLOCKS <= blocks_32 <= _CUS or _STREAM_32_TWO_ROUND_MIN_BLOCKS <= blocks_32 <= 2 * _CUS)
             and (K < _STREAM_DEEP_MIN_K or M >= _STREAM_32_LONG_K_MIN_M)):
         return _TILE_STREAM_32x64
     repeat_n, blocks = _stream_unsplit_shape(M, N)

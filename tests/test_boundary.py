@@ -493,8 +493,8 @@ def test_wide192_tile_rule():
 
 def test_stream32_tile_rule_for_m_over_64():
     """64 < M <= 512 on the streaming tiles with fp16 activations: the 32-row tile when it makes one round of 144-256 blocks
-    (it reads the weight half as often as the 16-row tiles); never with bf16 activations, which it widens per
-    fragment. Cells of the fitting sweep and of the held-out one."""
+    or two of 392-512 (it reads the weight half as often as the 16-row tiles); never with bf16 activations, which it
+    widens per fragment. Cells of the fitting sweep and of the held-out one."""
     from feather_ops.scaled_mm import select_scaled_mm_config as pick
 
     s32, s16 = (2, 2, 4, 2, 2, 0), (4, 1, 4, 1, 4, 0)
@@ -510,6 +510,11 @@ def test_stream32_tile_rule_for_m_over_64():
     assert pick(512, 1024, 1024) == s32        # 256 blocks: 1.16
     assert pick(384, 1280, 4096) == s32        # 240: 1.21
     assert pick(512, 1152, 1152) == s16        # 288 blocks, a second round: 0.91
+    assert pick(256, 2560, 2560) == s16        # 320 blocks: 0.96
+    assert pick(224, 3584, 3584) == s32        # 392 blocks, two rounds: 1.083
+    assert pick(256, 3584, 3584) == s32        # 448: 1.149
+    assert pick(512, 2048, 1024) == s32        # 512: 1.12
+    assert pick(512, 2048, 1024, torch.bfloat16) == s16
     assert pick(1024, 1024, 1024) != s32       # past the rows the sweeps covered
 
 

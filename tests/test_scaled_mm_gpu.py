@@ -221,6 +221,7 @@ HEURISTIC_CELLS = [
     (4112, 1024, 5120),  # 64 x 128 ring tile, one partial wave
     (512, 1024, 1024),   # 32-row streaming tile (fp16), 4-slice streaming tile (bf16)
     (384, 1280, 4096),   # 32-row streaming tile past 256 rows (fp16)
+    (512, 2048, 1024),   # 32-row streaming tile, two rounds of 256 blocks (fp16)
     (160, 1024, 8192),   # 16 x 64, 8 slices of unroll 1 (fp16) / 4 slices of unroll 2 (bf16): deep K
     (128, 2048, 8192),   # the same deep-K streaming tiles at 128 rows
     (80, 1024, 16384),   # 4-slice streaming tile split 3 ways (few ring tiles: not a ring split)
